@@ -1,0 +1,135 @@
+"""Drop-in Co-ALiBi attention for MI355X.
+
+Same public surface as the reference module co_alibi_attn/co_alibi_attn.py:
+``co_alibi_attention(q, k, v, causal=True, sm_scale=None, bias_max=8.0)``
+(reference :137-148), the autograd function ``CoALIBIAttention`` (:24-135) and
+the slope helper ``_get_coalibi_slopes`` (:11-22).  The work runs in the
+hand-written gfx950 kernels of ``libco_alibi.so`` (C ABI in include/co_alibi.h);
+grouped-query attention is handled inside the kernels instead of by
+``repeat_interleave``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native
+
+__all__ = ["co_alibi_attention", "CoALIBIAttention", "_get_coalibi_slopes"]
+
+
+def _get_coalibi_slopes(n_heads: int, bias_max: float = 8.0) -> torch.Tensor:
+    """ALiBi slopes with a configurable ``bias_max`` (reference co_alibi_attn.py:11-22).
+
+    With n the largest power of two <= n_heads, head h < n gets
+    2^(-bias_max*(h+1)/n); the remaining heads t = 0.. take the odd powers
+    2^(-(bias_max/2)*(2t+1)/n).  Computed with torch.pow on a float base and an
+    integer exponent tensor, so the values (default float dtype) are the
+    reference's bit for bit.
+    """
+    n = 1 << (int(n_heads).bit_length() - 1)
+    slopes = torch.pow(2.0 ** (-bias_max / n), torch.arange(1, n + 1))
+    extra = n_heads - n
+    if extra > 0:
+        odd_powers = torch.arange(1, 2 * extra, 2)
+        slopes = torch.cat([slopes, torch.pow(2.0 ** (-(bias_max / 2) / n), odd_powers)])
+    return slopes.abs()
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous tensor whose data pointer is 16-byte aligned (what the kernels load)."""
+    t = t.contiguous()
+    if t.data_ptr() % 16 != 0:
+        t = t.clone()
+    return t
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class CoALIBIAttention(torch.autograd.Function):
+    """Autograd function over the native forward / backward (reference co_alibi_attn.py:24-135).
+
+    ``apply(q, k, v, slopes, causal, sm_scale)``: q is (B, Hq, Sq, D); k and v
+    are (B, Hkv, Skv, D) with Hq a multiple of Hkv (Hkv == Hq is the
+    reference's only form); slopes holds Hq penalty slopes.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, slopes, causal, sm_scale):
+        batch_size, num_heads, seq_len_q, head_dim = q.shape
+        num_kv_heads, seq_len_kv = k.shape[1], k.shape[2]
+
+        assert num_kv_heads >= 1 and num_heads % num_kv_heads == 0
+        assert k.shape == (batch_size, num_kv_heads, seq_len_kv, head_dim)
+        assert v.shape == (batch_size, num_kv_heads, seq_len_kv, head_dim)
+        assert q.is_cuda and k.is_cuda and v.is_cuda, "Inputs must be CUDA tensors"
+        assert slopes.shape == (num_heads,), f"Slopes shape {slopes.shape} doesn't match num_heads {num_heads}"
+        if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _native.DTYPE_CODES:
+            raise TypeError(f"q, k, v must share one dtype of float32/float16/bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
+        if head_dim not in _native.SUPPORTED_HEAD_DIMS:
+            raise ValueError(f"head_dim must be one of {_native.SUPPORTED_HEAD_DIMS}, got {head_dim}")
+
+        q, k, v = _aligned(q), _aligned(k), _aligned(v)
+        slopes32 = slopes.detach().to(device=q.device, dtype=torch.float32).contiguous()
+        o = torch.empty_like(q)
+        lse = torch.empty((batch_size, num_heads, seq_len_q), device=q.device, dtype=torch.float32)
+        lib = _native.lib()
+        zb = torch.empty(
+            lib.co_alibi_zb_numel(batch_size, num_heads, seq_len_q, seq_len_kv),
+            device=q.device,
+            dtype=torch.float32,
+        )
+        with torch.cuda.device(q.device):
+            _native.check(
+                lib.co_alibi_fwd(
+                    _native.DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                    slopes32.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(),
+                    batch_size, num_heads, num_kv_heads, seq_len_q, seq_len_kv, head_dim,
+                    1 if causal else 0, float(sm_scale), _stream_handle(q.device),
+                )
+            )
+        ctx.save_for_backward(q, k, v, o, lse, zb, slopes32)
+        ctx.sm_scale = sm_scale
+        ctx.causal = causal
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse, zb, slopes32 = ctx.saved_tensors
+        batch_size, num_heads, seq_len_q, head_dim = q.shape
+        num_kv_heads, seq_len_kv = k.shape[1], k.shape[2]
+        do = _aligned(do.to(q.dtype))
+        dq = torch.empty_like(q)
+        dk = torch.empty_like(k)
+        dv = torch.empty_like(v)
+        lib = _native.lib()
+        ws_bytes = lib.co_alibi_bwd_workspace_bytes(batch_size, num_heads, seq_len_q, seq_len_kv)
+        workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
+        with torch.cuda.device(q.device):
+            _native.check(
+                lib.co_alibi_bwd(
+                    _native.DTYPE_CODES[q.dtype], do.data_ptr(), q.data_ptr(), k.data_ptr(),
+                    v.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), slopes32.data_ptr(),
+                    dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), workspace.data_ptr(), ws_bytes,
+                    batch_size, num_heads, num_kv_heads, seq_len_q, seq_len_kv, head_dim,
+                    1 if ctx.causal else 0, float(ctx.sm_scale), _stream_handle(q.device),
+                )
+            )
+        return dq, dk, dv, None, None, None
+
+
+def co_alibi_attention(q, k, v, causal=True, sm_scale=None, bias_max=8.0):
+    """Co-ALiBi attention (reference co_alibi_attn.py:137-148).
+
+    q: (B, Hq, Sq, D); k, v: (B, Hkv, Skv, D) with Hq a multiple of Hkv; query
+    head h uses key/value head h // (Hq // Hkv).  Returns (B, Hq, Sq, D) in
+    q.dtype.  ``sm_scale`` defaults to D**-0.5; the per-head slope is twice the
+    ALiBi slope of ``_get_coalibi_slopes(Hq, bias_max)``, rounded to q.dtype.
+    """
+    if sm_scale is None:
+        sm_scale = 1.0 / (q.shape[-1] ** 0.5)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    num_q_heads = q.shape[1]
+    slopes = (2.0 * _get_coalibi_slopes(num_q_heads, bias_max)).to(q.device, dtype=q.dtype)
+    return CoALIBIAttention.apply(q, k, v, slopes, causal, sm_scale)

@@ -1,0 +1,222 @@
+// C ABI entry points: argument checks, dtype / head-dim dispatch, launches.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/co_alibi.h"
+#include "coalibi_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+size_t num_zblocks(int seq_kv) { return (static_cast<size_t>(seq_kv) + 31) / 32; }
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+struct Shape {
+  int B, Hq, Hkv, Sq, Skv, D;
+};
+
+int check_shape(const char* fn, int dtype, const Shape& s) {
+  if (dtype != CO_ALIBI_F32 && dtype != CO_ALIBI_F16 && dtype != CO_ALIBI_BF16)
+    return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": dtype must be 0 (fp32), 1 (fp16) or 2 (bf16)");
+  if (s.B < 1 || s.Hq < 1 || s.Hkv < 1 || s.Sq < 1 || s.Skv < 1)
+    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": batch, heads and sequence lengths must be >= 1");
+  if (s.Hq % s.Hkv != 0)
+    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": heads_q must be a multiple of heads_kv");
+  if (s.D != 64 && s.D != 128)
+    return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": head_dim must be 64 or 128, got " + std::to_string(s.D));
+  // Sequence indices are 32-bit in the kernels; grids must fit a 31-bit launch.
+  const double wg = std::ceil(s.Sq / 128.0) * s.B * s.Hq;
+  if (s.Sq > (1 << 30) || s.Skv > (1 << 30) || wg > 2147483647.0)
+    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": problem too large for one launch");
+  return CO_ALIBI_OK;
+}
+
+int check_ptr(const char* fn, const char* name, const void* p, uintptr_t align) {
+  if (p == nullptr) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": " + name + " is NULL");
+  if (!aligned(p, align))
+    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": " + name + " is not " + std::to_string(align) + "-byte aligned");
+  return CO_ALIBI_OK;
+}
+
+template <typename T, int D>
+hipError_t fwd_dispatch_causal(const coalibi::FwdArgs& a, bool causal, hipStream_t st) {
+  return causal ? coalibi::launch_fwd<T, D, true>(a, st) : coalibi::launch_fwd<T, D, false>(a, st);
+}
+
+template <typename T>
+hipError_t fwd_dispatch_d(const coalibi::FwdArgs& a, int D, bool causal, hipStream_t st) {
+  return D == 64 ? fwd_dispatch_causal<T, 64>(a, causal, st) : fwd_dispatch_causal<T, 128>(a, causal, st);
+}
+
+template <typename T, int D>
+hipError_t bwd_dispatch_causal(const coalibi::BwdArgs& a, bool causal, int stages, hipStream_t st) {
+  return causal ? coalibi::launch_bwd<T, D, true>(a, stages, st) : coalibi::launch_bwd<T, D, false>(a, stages, st);
+}
+
+template <typename T>
+hipError_t bwd_dispatch_d(const coalibi::BwdArgs& a, int D, bool causal, int stages, hipStream_t st) {
+  return D == 64 ? bwd_dispatch_causal<T, 64>(a, causal, stages, st)
+                 : bwd_dispatch_causal<T, 128>(a, causal, stages, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t co_alibi_zb_numel(int batch, int heads_q, int seq_q, int seq_kv) {
+  if (batch < 1 || heads_q < 1 || seq_q < 1 || seq_kv < 1) return 0;
+  return static_cast<size_t>(batch) * heads_q * num_zblocks(seq_kv) * seq_q;
+}
+
+size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_kv) {
+  if (batch < 1 || heads_q < 1 || seq_q < 1 || seq_kv < 1) return 0;
+  const size_t rows = static_cast<size_t>(batch) * heads_q * seq_q;
+  return round_up(rows * sizeof(float), 256) + co_alibi_zb_numel(batch, heads_q, seq_q, seq_kv) * sizeof(float);
+}
+
+int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const float* slopes, void* o,
+                 float* lse, float* zb, int batch, int heads_q, int heads_kv, int seq_q, int seq_kv,
+                 int head_dim, int causal, float sm_scale, void* stream) {
+  const char* fn = "co_alibi_fwd";
+  const Shape s{batch, heads_q, heads_kv, seq_q, seq_kv, head_dim};
+  int rc;
+  if ((rc = check_shape(fn, dtype, s))) return rc;
+  if ((rc = check_ptr(fn, "q", q, 16)) || (rc = check_ptr(fn, "k", k, 16)) || (rc = check_ptr(fn, "v", v, 16)) ||
+      (rc = check_ptr(fn, "o", o, 16)) || (rc = check_ptr(fn, "slopes", slopes, 4)) ||
+      (rc = check_ptr(fn, "lse", lse, 4)) || (rc = check_ptr(fn, "zb", zb, 4)))
+    return rc;
+  if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, "co_alibi_fwd: sm_scale must be finite");
+
+  coalibi::FwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.slopes = slopes;
+  a.o = o;
+  a.lse = lse;
+  a.zb = zb;
+  a.B = batch;
+  a.Hq = heads_q;
+  a.Hkv = heads_kv;
+  a.Sq = seq_q;
+  a.Skv = seq_kv;
+  a.nZB = static_cast<int>(num_zblocks(seq_kv));
+  a.sc2 = sm_scale * coalibi::kLog2eHost;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (dtype) {
+    case CO_ALIBI_F16: e = fwd_dispatch_d<_Float16>(a, head_dim, causal != 0, st); break;
+    case CO_ALIBI_BF16: e = fwd_dispatch_d<__bf16>(a, head_dim, causal != 0, st); break;
+    default: e = fwd_dispatch_d<float>(a, head_dim, causal != 0, st); break;
+  }
+  if (e != hipSuccess) return fail(CO_ALIBI_ELAUNCH, std::string("co_alibi_fwd: launch failed: ") + hipGetErrorString(e));
+  return CO_ALIBI_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// stages: 1 = pass 1 (dq, dsum, cb), 2 = pass 2 (dk, dv), 3 = both.
+int bwd_impl(const char* fn, int stages, int dtype, const void* dout, const void* q, const void* k,
+             const void* v, const void* o, const float* lse, const float* zb, const float* slopes, void* dq,
+             void* dk, void* dv, void* workspace, size_t workspace_bytes, int batch, int heads_q,
+             int heads_kv, int seq_q, int seq_kv, int head_dim, int causal, float sm_scale, void* stream) {
+  const Shape s{batch, heads_q, heads_kv, seq_q, seq_kv, head_dim};
+  int rc;
+  if ((rc = check_shape(fn, dtype, s))) return rc;
+  if ((rc = check_ptr(fn, "dout", dout, 16)) || (rc = check_ptr(fn, "q", q, 16)) ||
+      (rc = check_ptr(fn, "k", k, 16)) || (rc = check_ptr(fn, "v", v, 16)) ||
+      (rc = check_ptr(fn, "lse", lse, 4)) || (rc = check_ptr(fn, "zb", zb, 4)) ||
+      (rc = check_ptr(fn, "slopes", slopes, 4)) || (rc = check_ptr(fn, "workspace", workspace, 256)))
+    return rc;
+  if ((stages & 1) && ((rc = check_ptr(fn, "o", o, 16)) || (rc = check_ptr(fn, "dq", dq, 16)))) return rc;
+  if ((stages & 2) && ((rc = check_ptr(fn, "dk", dk, 16)) || (rc = check_ptr(fn, "dv", dv, 16)))) return rc;
+  const size_t need = co_alibi_bwd_workspace_bytes(batch, heads_q, seq_q, seq_kv);
+  if (workspace_bytes < need)
+    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": workspace of " + std::to_string(workspace_bytes) +
+                                     " bytes, need " + std::to_string(need));
+  if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": sm_scale must be finite");
+
+  const size_t rows = static_cast<size_t>(batch) * heads_q * seq_q;
+  coalibi::BwdArgs a{};
+  a.dout = dout;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.zb = zb;
+  a.slopes = slopes;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.dsum = static_cast<float*>(workspace);
+  a.cb = reinterpret_cast<float*>(static_cast<char*>(workspace) + round_up(rows * sizeof(float), 256));
+  a.B = batch;
+  a.Hq = heads_q;
+  a.Hkv = heads_kv;
+  a.Sq = seq_q;
+  a.Skv = seq_kv;
+  a.nZB = static_cast<int>(num_zblocks(seq_kv));
+  a.sc2 = sm_scale * coalibi::kLog2eHost;
+  a.sm_scale = sm_scale;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (dtype) {
+    case CO_ALIBI_F16: e = bwd_dispatch_d<_Float16>(a, head_dim, causal != 0, stages, st); break;
+    case CO_ALIBI_BF16: e = bwd_dispatch_d<__bf16>(a, head_dim, causal != 0, stages, st); break;
+    default: e = bwd_dispatch_d<float>(a, head_dim, causal != 0, stages, st); break;
+  }
+  if (e != hipSuccess) return fail(CO_ALIBI_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return CO_ALIBI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int co_alibi_bwd(int dtype, const void* dout, const void* q, const void* k, const void* v, const void* o,
+                 const float* lse, const float* zb, const float* slopes, void* dq, void* dk, void* dv,
+                 void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv, int seq_q,
+                 int seq_kv, int head_dim, int causal, float sm_scale, void* stream) {
+  return bwd_impl("co_alibi_bwd", 3, dtype, dout, q, k, v, o, lse, zb, slopes, dq, dk, dv, workspace,
+                  workspace_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal, sm_scale, stream);
+}
+
+int co_alibi_bwd_dq(int dtype, const void* dout, const void* q, const void* k, const void* v, const void* o,
+                    const float* lse, const float* zb, const float* slopes, void* dq, void* workspace,
+                    size_t workspace_bytes, int batch, int heads_q, int heads_kv, int seq_q, int seq_kv,
+                    int head_dim, int causal, float sm_scale, void* stream) {
+  return bwd_impl("co_alibi_bwd_dq", 1, dtype, dout, q, k, v, o, lse, zb, slopes, dq, nullptr, nullptr,
+                  workspace, workspace_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal,
+                  sm_scale, stream);
+}
+
+int co_alibi_bwd_dkdv(int dtype, const void* dout, const void* q, const void* k, const void* v,
+                      const float* lse, const float* zb, const float* slopes, void* dk, void* dv,
+                      void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv,
+                      int seq_q, int seq_kv, int head_dim, int causal, float sm_scale, void* stream) {
+  return bwd_impl("co_alibi_bwd_dkdv", 2, dtype, dout, q, k, v, nullptr, lse, zb, slopes, nullptr, dk, dv,
+                  workspace, workspace_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal,
+                  sm_scale, stream);
+}
+
+const char* co_alibi_last_error(void) { return g_last_error.c_str(); }
+
+int co_alibi_abi_version(void) { return 1; }
+
+}  // extern "C"

@@ -1,0 +1,197 @@
+// Shared device helpers for the Co-ALiBi gfx950 kernels.
+//
+// Matrix products run on CDNA4 MFMA 32x32 tiles.  A "k16 step" is one
+// 32x32x16 product: each lane supplies 8 consecutive elements of the
+// reduction axis for A and for B (lane l: row/col l%32, reduction half l/32).
+// fp16/bf16 use one v_mfma_f32_32x32x16_{f16,bf16}; fp32 (the validation
+// mode) issues eight v_mfma_f32_32x32x2_f32, one per element, which reduces
+// over the same 16 values because the same (lane, element) -> k assignment is
+// used for both operands.
+//
+// Accumulator layout of a 32x32 tile (16 fp32 per lane): register r of lane l
+// holds row (r/4)*8 + (l/32)*4 + (r%4), column l%32.  The kernels read the A
+// rows through the permutation kRowOfReg below so that register r of lane l
+// holds logical row (l/32)*16 + r: every lane then owns 16 consecutive rows,
+// which is what makes the key-axis scans of Co-ALiBi register-local.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace coalibi {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+template <typename T> struct Mfma;
+
+template <> struct Mfma<_Float16> {
+  using vec8 = f16x8;
+  static __device__ __forceinline__ f32x16 k16(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ vec8 pack(f32x8 x) { return __builtin_convertvector(x, vec8); }
+};
+
+template <> struct Mfma<__bf16> {
+  using vec8 = bf16x8;
+  static __device__ __forceinline__ f32x16 k16(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ vec8 pack(f32x8 x) { return __builtin_convertvector(x, vec8); }
+};
+
+template <> struct Mfma<float> {
+  using vec8 = f32x8;
+  static __device__ __forceinline__ f32x16 k16(vec8 a, vec8 b, f32x16 c) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], b[e], c, 0, 0, 0);
+    return c;
+  }
+  static __device__ __forceinline__ vec8 pack(f32x8 x) { return x; }
+};
+
+// Logical row held by MFMA row R (0..31) when A rows are permuted so that
+// accumulator register r of lane l holds logical row (l/32)*16 + r.
+__device__ __forceinline__ constexpr int kRowOfReg(int R) {
+  return ((R >> 2) & 1) * 16 + (R >> 3) * 4 + (R & 3);
+}
+// Inverse: the MFMA row that must hold logical row k (0..31).
+__host__ __device__ __forceinline__ constexpr int kRegOfRow(int k) {
+  return ((k >> 2) & 3) * 8 + ((k >> 4) & 1) * 4 + (k & 3);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// sigma(p) with t = p*log2(e):  1 / (1 + 2^-t)
+__device__ __forceinline__ float sigmoid_log2(float t) { return fast_rcp(1.0f + fast_exp2(-t)); }
+
+// Value held by the lane in the other half of the wavefront (l ^ 32).
+__device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32); }
+
+// Inclusive prefix sum across the 32 lanes of each wavefront half
+// (lanes 0..31 and 32..63 are independent segments).
+__device__ __forceinline__ float half_wave_prefix(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));  // row_shr:1
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, true));  // row_shr:2
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, true));  // row_shr:4
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, true));  // row_shr:8
+  // row_bcast:15 into rows 1 and 3: lanes 16..31 (48..63) add lane 15 (47).
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));
+  return x;
+}
+
+// 16-byte global / LDS accessors.
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::vec8 ld_vec8(const T* p) {
+  return *reinterpret_cast<const typename Mfma<T>::vec8*>(p);
+}
+
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::vec8 zero_vec8() {
+  typename Mfma<T>::vec8 z;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) z[e] = T(0);
+  return z;
+}
+
+// Work-group id -> logical work item.  Consecutive work-group ids are
+// dispatched round-robin over the 8 XCDs; this remap makes consecutive logical
+// items run on the same XCD so that the tiles sharing one head's K/V (or Q/dO)
+// are served from one L2.
+__device__ __forceinline__ int xcd_remap(int id, int n) {
+  constexpr int kXcd = 8;
+  if (n % kXcd != 0) return id;
+  return (id % kXcd) * (n / kXcd) + id / kXcd;
+}
+
+}  // namespace coalibi
+
+namespace coalibi {
+
+template <typename T, int N> struct VecOf { typedef T type __attribute__((ext_vector_type(N))); };
+
+// Stages a ROWS x D tile of a row-major [rows][D] matrix through registers into
+// LDS.  Each thread owns KG consecutive rows x one 16-byte column chunk, so the
+// same registers can be written both row-major (store_rows: rows permuted with
+// kRegOfRow inside every 32-row block, the layout the A operand of a
+// "rows along registers" product reads) and transposed (store_cols: the
+// [D][rows] layout the A operand of a "reduce over rows" product reads).
+// Rows at or beyond `nrows` read as zero.
+template <typename T, int D, int ROWS>
+struct TileLoader {
+  static constexpr int CH = 16 / sizeof(T);                       // elements per chunk
+  static constexpr int KG = ((ROWS / 4) * (D / CH) >= 256) ? 4 : 2;  // rows per thread group
+  static constexpr int NG = (ROWS / KG) * (D / CH);                // groups per tile
+  static constexpr int GPT = NG / 256;                             // groups per thread
+  static_assert(NG % 256 == 0 && GPT >= 1, "tile does not split over 256 threads");
+  static_assert(ROWS % 32 == 0, "rows are permuted in blocks of 32");
+
+  u32x4 r[GPT][KG];
+
+  __device__ __forceinline__ static int grp_row(int g) { return (g % (ROWS / KG)) * KG; }
+  __device__ __forceinline__ static int grp_col(int g) { return (g / (ROWS / KG)) * CH; }
+
+  __device__ __forceinline__ void load(const T* __restrict__ base, int row0, int nrows, int tid) {
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int g = tid + 256 * i;
+      const int rr = grp_row(g), cc = grp_col(g);
+#pragma unroll
+      for (int k = 0; k < KG; ++k) {
+        const int row = row0 + rr + k;
+        r[i][k] = row < nrows ? ld16(base + (size_t)row * D + cc) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  }
+
+  // s[R * ld + c] with R = (row & ~31) | kRegOfRow(row & 31)
+  __device__ __forceinline__ void store_rows(T* s, int ld, int tid) const {
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int g = tid + 256 * i;
+      const int rr = grp_row(g), cc = grp_col(g);
+#pragma unroll
+      for (int k = 0; k < KG; ++k) {
+        const int row = rr + k;
+        const int R = (row & ~31) | kRegOfRow(row & 31);
+        st16(s + R * ld + cc, r[i][k]);
+      }
+    }
+  }
+
+  // s[c * ld + row] (rows in natural order)
+  __device__ __forceinline__ void store_cols(T* s, int ld, int tid) const {
+    using chunk = typename VecOf<T, CH>::type;
+    using grp = typename VecOf<T, KG>::type;
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int g = tid + 256 * i;
+      const int rr = grp_row(g), cc = grp_col(g);
+      chunk rows[KG];
+#pragma unroll
+      for (int k = 0; k < KG; ++k) rows[k] = __builtin_bit_cast(chunk, r[i][k]);
+#pragma unroll
+      for (int e = 0; e < CH; ++e) {
+        grp w;
+#pragma unroll
+        for (int k = 0; k < KG; ++k) w[k] = rows[k][e];
+        *reinterpret_cast<grp*>(s + (cc + e) * ld + rr) = w;
+      }
+    }
+  }
+};
+
+}  // namespace coalibi

@@ -1,0 +1,267 @@
+// Co-ALiBi forward on gfx950.
+//
+// Semantics follow the reference forward (co_alibi_attn/co_alibi_fwd_kernel.py:46-127
+// and model.py:13-40 with the per-head slope of co_alibi_attn.py:147):
+//   p_ij   = sm_scale * q_i . k_j
+//   s_ij   = sigmoid(p_ij) for valid (i, j), else 0     valid: j < Skv and (!causal or j <= i)
+//   z_ij   = sum_{k >= j} s_ik                          (inclusive suffix over keys)
+//   a_ij   = p_ij - slope_h * z_ij
+//   O_i    = sum_j exp(a_ij - m_i) v_j / (sum_j exp(a_ij - m_i) + 1e-9)
+//   LSE_i  = m_i + log(sum_j exp(a_ij - m_i) + 1e-9)
+//
+// One work-group = 128 query rows of one (batch, query head), 4 wavefronts of
+// 32 rows.  Key tiles of 64 are walked from the causal diagonal leftwards so
+// the suffix sum z is a running carry.  Per tile and wavefront:
+//   S^T = K Q^T   (MFMA, keys on the accumulator rows: with the kRowOfReg
+//                  permutation each lane holds 16 consecutive keys of one row)
+//   sigmoid, suffix scan (in registers + one exchange with the other half),
+//   penalty, online softmax (exp2, lazily rescaled), then
+//   O^T += V^T P^T (MFMA, the P accumulators are reused as the B operand).
+// K is staged in LDS row-major (rows permuted), V transposed ([d][key]).
+// Besides O and LSE the kernel writes zb: the suffix sum at every 32-key block
+// start, the only penalty statistic the backward needs.
+#include "coalibi_common.h"
+#include "coalibi_kernels.h"
+
+namespace coalibi {
+
+namespace {
+
+constexpr int kFwdBM = 128;  // query rows per work-group
+constexpr int kFwdBN = 64;   // keys per tile
+// Rescale O only when the running max grows by more than 2^8: P stays <= 256,
+// exact in fp16/bf16 range, and O/LSE are renormalised to the true max at the end.
+constexpr float kRescaleThreshold = 8.0f;
+
+template <typename T, int D>
+struct FwdCfg {
+  static constexpr int CH = 16 / sizeof(T);
+  static constexpr int LDK = D + CH;       // sK row stride (elements)
+  static constexpr int LDV = kFwdBN + CH;  // sVt row stride
+  static constexpr int KS = D / 16;        // k16 steps over the head dim
+  static constexpr int DT = D / 32;        // 32-row tiles of O^T
+};
+
+template <bool MASKED, bool CAUSAL>
+__device__ __forceinline__ bool key_ok(int key, int row, int Skv) {
+  if (!MASKED) return true;
+  return key < Skv && (!CAUSAL || key <= row);
+}
+
+template <typename T, int D, bool CAUSAL, bool MASKED>
+__device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __restrict__ sVt,
+                                         const typename Mfma<T>::vec8 (&qf)[FwdCfg<T, D>::KS],
+                                         f32x16 (&acc)[FwdCfg<T, D>::DT], float& m2, float& mtrue,
+                                         float& lsum, float& zr, float& zst0, float& zst1, int k0,
+                                         int row, int col, int hh, int Skv, float sc2, float lam2) {
+  using C = FwdCfg<T, D>;
+  using M = Mfma<T>;
+
+  // S^T tile: two 32-key subtiles; register r of subtile st <-> key k0 + st*32 + hh*16 + r.
+  f32x16 sacc[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    sacc[st] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks)
+      sacc[st] = M::k16(ld_vec8(sK + (st * 32 + col) * C::LDK + ks * 16 + hh * 8), qf[ks], sacc[st]);
+  }
+
+  __builtin_amdgcn_sched_barrier(0);
+  // In place: sacc becomes t = p*log2(e), then the log2-domain logit a.
+  float sg[2][16];
+  float tot[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    float sum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float tv = sacc[st][r] * sc2;
+      float s = sigmoid_log2(tv);
+      if (MASKED) s = key_ok<MASKED, CAUSAL>(k0 + st * 32 + hh * 16 + r, row, Skv) ? s : 0.f;
+      sacc[st][r] = tv;
+      sg[st][r] = s;
+      sum += s;
+    }
+    tot[st] = sum;
+  }
+  // Run totals in key order (right to left): (1,1) (1,0) (0,1) (0,0), where (st, h) is
+  // the 16-key run of subtile st held by wavefront half h.
+  const float oth0 = other_half(tot[0]), oth1 = other_half(tot[1]);
+  const float T11 = hh ? tot[1] : oth1, T10 = hh ? oth1 : tot[1];
+  const float T01 = hh ? tot[0] : oth0, T00 = hh ? oth0 : tot[0];
+  zst1 = (zr + T11) + T10;    // suffix sum from key k0 + 32
+  zst0 = (zst1 + T01) + T00;  // suffix sum from key k0
+  const float off[2] = {hh ? zst1 : zst1 + T01, hh ? zr : zr + T11};
+  zr = zst0;
+
+  float mt = kNegInf;
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    float run = off[st];
+#pragma unroll
+    for (int r = 15; r >= 0; --r) {
+      run += sg[st][r];
+      float av = sacc[st][r] - lam2 * run;
+      if (MASKED) av = key_ok<MASKED, CAUSAL>(k0 + st * 32 + hh * 16 + r, row, Skv) ? av : kNegInf;
+      sacc[st][r] = av;
+      mt = fmaxf(mt, av);
+    }
+  }
+  mt = fmaxf(mt, other_half(mt));
+  mtrue = fmaxf(mtrue, mt);
+  const bool need = mt > m2 + kRescaleThreshold;
+  if (__any(need)) {
+    const float alpha = need ? fast_exp2(m2 - mt) : 1.f;
+    m2 = need ? mt : m2;
+    lsum *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
+  }
+  const float mb = m2 == kNegInf ? 0.f : m2;
+
+  typename M::vec8 pb[2][2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+#pragma unroll
+    for (int mh = 0; mh < 2; ++mh) {
+      f32x8 pv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float p = fast_exp2(sacc[st][mh * 8 + e] - mb);
+        lsum += p;
+        pv[e] = p;
+      }
+      pb[st][mh] = M::pack(pv);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // O^T[d][q] += V^T[d][key] P^T[key][q]
+#pragma unroll
+  for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh)
+        acc[dt] = M::k16(ld_vec8(sVt + (dt * 32 + col) * C::LDV + st * 32 + hh * 16 + mh * 8),
+                         pb[st][mh], acc[dt]);
+    }
+  }
+}
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kernel(FwdArgs args) {
+  using C = FwdCfg<T, D>;
+  using M = Mfma<T>;
+  using vec8 = typename M::vec8;
+  using Tile = TileLoader<T, D, kFwdBN>;
+  __shared__ __align__(16) T sK[kFwdBN * C::LDK];
+  __shared__ __align__(16) T sVt[D * C::LDV];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 31, hh = lane >> 5;
+  const int Sq = args.Sq, Skv = args.Skv;
+  const int nQB = (Sq + kFwdBM - 1) / kFwdBM;
+  const int wid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = wid / nQB;
+  const int qb = nQB - 1 - (wid - bh * nQB);  // longest causal rows first
+  const int b = bh / args.Hq, hq = bh - b * args.Hq;
+  const int hkv = hq / (args.Hq / args.Hkv);
+  const T* __restrict__ Qp = static_cast<const T*>(args.q) + (size_t)bh * Sq * D;
+  const size_t kvoff = ((size_t)b * args.Hkv + hkv) * (size_t)Skv * D;
+  const T* __restrict__ Kp = static_cast<const T*>(args.k) + kvoff;
+  const T* __restrict__ Vp = static_cast<const T*>(args.v) + kvoff;
+  const float lam2 = args.slopes[hq] * kLog2e;
+  const float sc2 = args.sc2;
+
+  const int q0 = qb * kFwdBM;
+  const int wrow0 = q0 + wave * 32;
+  const int row = wrow0 + col;
+  const bool row_ok = row < Sq;
+
+  vec8 qf[C::KS];
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks)
+    qf[ks] = row_ok ? ld_vec8(Qp + (size_t)row * D + ks * 16 + hh * 8) : zero_vec8<T>();
+
+  const int last_key = CAUSAL ? min(q0 + kFwdBM - 1, Skv - 1) : Skv - 1;
+  const int nkt = last_key / kFwdBN + 1;
+
+  Tile kt_regs, vt_regs;
+  kt_regs.load(Kp, (nkt - 1) * kFwdBN, Skv, tid);
+  vt_regs.load(Vp, (nkt - 1) * kFwdBN, Skv, tid);
+
+  f32x16 acc[C::DT];
+#pragma unroll
+  for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
+  float m2 = kNegInf, mtrue = kNegInf, lsum = 0.f, zr = 0.f;
+  float* __restrict__ zb_row = args.zb + (size_t)bh * args.nZB * Sq + row;
+
+  for (int kt = nkt - 1; kt >= 0; --kt) {
+    __syncthreads();
+    kt_regs.store_rows(sK, C::LDK, tid);
+    vt_regs.store_cols(sVt, C::LDV, tid);
+    __syncthreads();
+    if (kt > 0) {
+      kt_regs.load(Kp, (kt - 1) * kFwdBN, Skv, tid);
+      vt_regs.load(Vp, (kt - 1) * kFwdBN, Skv, tid);
+    }
+    const int k0 = kt * kFwdBN;
+    if (CAUSAL && k0 > wrow0 + 31) continue;  // every key of the tile is above this wavefront's rows
+    const bool masked = (CAUSAL && k0 + kFwdBN - 1 > wrow0) || (k0 + kFwdBN > Skv);
+    float zst0, zst1;
+    if (masked)
+      fwd_tile<T, D, CAUSAL, true>(sK, sVt, qf, acc, m2, mtrue, lsum, zr, zst0, zst1, k0, row, col, hh,
+                                   Skv, sc2, lam2);
+    else
+      fwd_tile<T, D, CAUSAL, false>(sK, sVt, qf, acc, m2, mtrue, lsum, zr, zst0, zst1, k0, row, col, hh,
+                                    Skv, sc2, lam2);
+    if (hh == 0 && row_ok) {
+      zb_row[(size_t)(2 * kt) * Sq] = zst0;
+      if (k0 + 32 < Skv) zb_row[(size_t)(2 * kt + 1) * Sq] = zst1;
+    }
+  }
+
+  // Renormalise to the true row max: l_true = l * 2^(m2 - mtrue).
+  const float ltot = lsum + other_half(lsum);
+  const float c = m2 == kNegInf ? 0.f : fast_exp2(m2 - mtrue);
+  const float ltrue = ltot * c;
+  const float inv = c / (ltrue + 1e-9f);
+  if (row_ok) {
+    T* __restrict__ Orow = static_cast<T*>(args.o) + ((size_t)bh * Sq + row) * D;
+    using vec4 = typename VecOf<T, 4>::type;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4 v4 = {acc[dt][g * 4 + 0] * inv, acc[dt][g * 4 + 1] * inv, acc[dt][g * 4 + 2] * inv,
+                    acc[dt][g * 4 + 3] * inv};
+        *reinterpret_cast<vec4*>(Orow + dt * 32 + g * 8 + hh * 4) = __builtin_convertvector(v4, vec4);
+      }
+    }
+    if (hh == 0) args.lse[(size_t)bh * Sq + row] = (mtrue + log2f(ltrue + 1e-9f)) * kLn2;
+  }
+}
+
+}  // namespace
+
+template <typename T, int D, bool CAUSAL>
+hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
+  const int nQB = (a.Sq + kFwdBM - 1) / kFwdBM;
+  const int grid = nQB * a.B * a.Hq;
+  hipLaunchKernelGGL((coalibi_fwd_kernel<T, D, CAUSAL>), dim3(grid), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+#define COALIBI_INST_FWD(T, D)                                           \
+  template hipError_t launch_fwd<T, D, true>(const FwdArgs&, hipStream_t); \
+  template hipError_t launch_fwd<T, D, false>(const FwdArgs&, hipStream_t);
+
+COALIBI_INST_FWD(_Float16, 64)
+COALIBI_INST_FWD(_Float16, 128)
+COALIBI_INST_FWD(__bf16, 64)
+COALIBI_INST_FWD(__bf16, 128)
+COALIBI_INST_FWD(float, 64)
+COALIBI_INST_FWD(float, 128)
+
+}  // namespace coalibi

@@ -1,0 +1,96 @@
+/*
+ * co_alibi.h - C ABI of the MI355X (gfx950) Co-ALiBi attention library.
+ *
+ * The library holds the two hot-path launches of the reference
+ * (Nathancgy/Co-ALIBI) behind plain pointers and sizes:
+ *
+ *   co_alibi_fwd  replaces the forward launch `_co_alibi_fwd_kernel[grid](...)`
+ *                 in co_alibi_attn/co_alibi_attn.py:41-57 (and the O / LSE /
+ *                 RowSigTotal allocations at :35-37 move to the caller).
+ *   co_alibi_bwd  replaces the backward launch `_co_alibi_bwd_kernel[grid](...)`
+ *                 in co_alibi_attn/co_alibi_attn.py:101-123 together with the
+ *                 dK/dV partial buffers and their reduction (:83-99, :132-133).
+ *
+ * Tensor layout: contiguous row-major, q / o / dout / dq are (B, Hq, Sq, D),
+ * k / v / dk / dv are (B, Hkv, Skv, D); query head h attends key/value head
+ * h / (Hq / Hkv) (the head mapping of co_alibi_attn.py:143-146, done in-kernel
+ * instead of by repeat_interleave).  Element type is selected by `dtype`; all
+ * statistics are fp32.  `slopes` holds Hq fp32 penalty slopes (the caller
+ * rounds them to the input dtype first, as co_alibi_attn.py:147 does).
+ * Causal masking is top-left aligned (key j is visible to query i iff j <= i).
+ *
+ * Every call is asynchronous on `stream` (a hipStream_t; NULL = the null
+ * stream), allocates nothing, and returns CO_ALIBI_OK or an error code; the
+ * message of the last failure on the calling thread is co_alibi_last_error().
+ * Pointers to element data must be 16-byte aligned, fp32 arrays 4-byte aligned.
+ */
+#ifndef CO_ALIBI_H
+#define CO_ALIBI_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum co_alibi_dtype { CO_ALIBI_F32 = 0, CO_ALIBI_F16 = 1, CO_ALIBI_BF16 = 2 };
+
+enum co_alibi_status {
+  CO_ALIBI_OK = 0,
+  CO_ALIBI_EINVAL = 1,       /* bad pointer, size, alignment or workspace */
+  CO_ALIBI_EUNSUPPORTED = 2, /* dtype or head_dim without a kernel */
+  CO_ALIBI_ELAUNCH = 3       /* the HIP runtime refused the launch */
+};
+
+/* Number of fp32 elements of the penalty statistics `zb` that co_alibi_fwd
+ * writes and co_alibi_bwd reads: B*Hq * ceil(Skv/32) * Sq.  zb[bh][J][i] is the
+ * sum of sigmoid(sm_scale * q_i.k_j) over the visible keys j >= 32*J of row i.
+ * It takes the place of the reference's RowSigTotal (co_alibi_attn.py:37). */
+size_t co_alibi_zb_numel(int batch, int heads_q, int seq_q, int seq_kv);
+
+/* Bytes of device scratch co_alibi_bwd needs. */
+size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_kv);
+
+/* Forward: writes o (B,Hq,Sq,D, dtype), lse (B,Hq,Sq, fp32 natural log-sum-exp,
+ * m_i + log(l_i + 1e-9) as co_alibi_fwd_kernel.py:120) and zb. */
+int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const float* slopes,
+                 void* o, float* lse, float* zb, int batch, int heads_q, int heads_kv, int seq_q,
+                 int seq_kv, int head_dim, int causal, float sm_scale, void* stream);
+
+/* Backward: given dout and the forward's q, k, v, o, lse, zb, writes dq
+ * (B,Hq,Sq,D), dk and dv (B,Hkv,Skv,D), all in dtype.  For Hkv < Hq the key /
+ * value gradients are summed over the query heads of each group.  workspace
+ * must hold co_alibi_bwd_workspace_bytes(...) bytes (256-byte aligned). */
+int co_alibi_bwd(int dtype, const void* dout, const void* q, const void* k, const void* v,
+                 const void* o, const float* lse, const float* zb, const float* slopes, void* dq,
+                 void* dk, void* dv, void* workspace, size_t workspace_bytes, int batch, int heads_q,
+                 int heads_kv, int seq_q, int seq_kv, int head_dim, int causal, float sm_scale,
+                 void* stream);
+
+/* The two passes of co_alibi_bwd as separate calls, for callers that time or
+ * schedule them apart.  co_alibi_bwd_dq writes dq and fills the workspace
+ * (per-row dO.O and the per-32-key-block prefix of dA); co_alibi_bwd_dkdv
+ * then writes dk and dv from that workspace.  Issued in this order on one
+ * stream they are exactly co_alibi_bwd.  The reference runs both in one
+ * kernel (co_alibi_attn/co_alibi_bwd_kernel.py:17-146). */
+int co_alibi_bwd_dq(int dtype, const void* dout, const void* q, const void* k, const void* v,
+                    const void* o, const float* lse, const float* zb, const float* slopes, void* dq,
+                    void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv,
+                    int seq_q, int seq_kv, int head_dim, int causal, float sm_scale, void* stream);
+
+int co_alibi_bwd_dkdv(int dtype, const void* dout, const void* q, const void* k, const void* v,
+                      const float* lse, const float* zb, const float* slopes, void* dk, void* dv,
+                      void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv,
+                      int seq_q, int seq_kv, int head_dim, int causal, float sm_scale, void* stream);
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* co_alibi_last_error(void);
+
+/* ABI version of this header: 1. */
+int co_alibi_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CO_ALIBI_H */

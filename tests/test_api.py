@@ -1,0 +1,109 @@
+"""Host-side behaviour that needs no GPU: the C ABI library, argument checks, the drop-in surface."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import co_alibi_attn
+from co_alibi_attn import _native
+from co_alibi_attn.co_alibi_attn import CoALIBIAttention, _get_coalibi_slopes
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "co_alibi.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:size_t|int|const char\*)\s+(co_alibi_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed from include/co_alibi.h"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in co_alibi.h but not exported"
+    assert sorted(_native.EXPORTS) == declared
+    assert lib.co_alibi_abi_version() == 1
+
+
+def test_sizes():
+    lib = _native.lib()
+    # zb: B*Hq*ceil(Skv/32)*Sq fp32
+    assert lib.co_alibi_zb_numel(4, 16, 4096, 4096) == 4 * 16 * 128 * 4096
+    assert lib.co_alibi_zb_numel(1, 2, 5, 33) == 1 * 2 * 2 * 5
+    assert lib.co_alibi_zb_numel(0, 2, 5, 33) == 0
+    rows = 4 * 16 * 4096
+    assert lib.co_alibi_bwd_workspace_bytes(4, 16, 4096, 4096) == rows * 4 + 4 * 16 * 128 * 4096 * 4
+    assert lib.co_alibi_bwd_workspace_bytes(1, 1, 3, 3) == 256 + 1 * 1 * 1 * 3 * 4
+
+
+def _fwd(lib, **over):
+    args = dict(dtype=1, q=16, k=16, v=16, slopes=16, o=16, lse=16, zb=16, B=1, Hq=2, Hkv=2, Sq=8, Skv=8,
+                D=64, causal=1, scale=0.125)
+    args.update(over)
+    return lib.co_alibi_fwd(args["dtype"], args["q"], args["k"], args["v"], args["slopes"], args["o"],
+                            args["lse"], args["zb"], args["B"], args["Hq"], args["Hkv"], args["Sq"],
+                            args["Skv"], args["D"], args["causal"], args["scale"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(q=None), 1, "q is NULL"),
+    (dict(k=24), 1, "k is not 16-byte aligned"),
+    (dict(lse=2), 1, "lse is not 4-byte aligned"),
+    (dict(D=96), 2, "head_dim must be 64 or 128"),
+    (dict(dtype=7), 2, "dtype must be"),
+    (dict(Hq=3, Hkv=2), 1, "multiple of heads_kv"),
+    (dict(Sq=0), 1, ">= 1"),
+    (dict(scale=float("nan")), 1, "sm_scale must be finite"),
+])
+def test_fwd_argument_errors(over, code, msg):
+    lib = _native.lib()
+    assert _fwd(lib, **over) == code
+    assert msg in lib.co_alibi_last_error().decode()
+
+
+def test_bwd_argument_errors():
+    lib = _native.lib()
+    P = 256
+    rc = lib.co_alibi_bwd(1, P, P, P, P, P, P, P, P, P, P, P, P, 0, 1, 2, 2, 8, 8, 64, 1, 0.125, None)
+    assert rc == 1 and "workspace of 0 bytes" in lib.co_alibi_last_error().decode()
+    rc = lib.co_alibi_bwd_dkdv(1, P, P, P, P, P, P, P, None, P, P, 1 << 20, 1, 2, 2, 8, 8, 64, 1, 0.125, None)
+    assert rc == 1 and "dk is NULL" in lib.co_alibi_last_error().decode()
+    # pass 1 does not need dk / dv
+    rc = lib.co_alibi_bwd_dq(1, P, P, P, P, P, P, P, P, None, P, 1 << 20, 1, 2, 2, 8, 8, 64, 1, 0.125, None)
+    assert rc == 1 and "dq is NULL" in lib.co_alibi_last_error().decode()
+
+
+def test_public_surface_matches_reference():
+    assert co_alibi_attn.__all__ == ["co_alibi_attention"]
+    import inspect
+    sig = inspect.signature(co_alibi_attn.co_alibi_attention)
+    assert list(sig.parameters) == ["q", "k", "v", "causal", "sm_scale", "bias_max"]
+    assert sig.parameters["causal"].default is True
+    assert sig.parameters["sm_scale"].default is None
+    assert sig.parameters["bias_max"].default == 8.0
+
+
+def test_cpu_tensors_rejected_like_reference():
+    q = torch.randn(1, 2, 8, 64)
+    with pytest.raises(AssertionError, match="CUDA"):
+        co_alibi_attn.co_alibi_attention(q, q, q)
+
+
+def test_shape_asserts():
+    q = torch.randn(1, 4, 8, 64)
+    k = torch.randn(1, 3, 8, 64)  # 4 query heads cannot share 3 key heads
+    with pytest.raises(AssertionError):
+        co_alibi_attn.co_alibi_attention(q, k, k)
+    with pytest.raises(AssertionError):
+        CoALIBIAttention.apply(q, q, q, torch.ones(3), True, 0.1)  # slope count
+
+
+def test_slopes_dtype_rounding():
+    s16 = (2.0 * _get_coalibi_slopes(16)).to(torch.float16)
+    # 2^(0.5 - h/2): odd h are exact powers of two, even h round in fp16
+    assert s16[1].item() == 1.0 and s16[15].item() == 2.0 ** -7
+    assert abs(s16[0].item() - 2 ** 0.5) < 2 ** 0.5 * 2 ** -11

@@ -1,0 +1,241 @@
+"""HIP kernels vs the CPU oracle (the parity gate).  Needs an MI355X.
+
+Bar: max-abs <= 1e-4 in the fp32 validation mode,
+<= 2e-2 for O, dQ, dK, dV with fp16/bf16 inputs, against the oracle run in
+fp32 on the same (dtype-rounded) inputs with the same dtype-rounded slopes.
+Every GPU call goes through the C ABI (directly, or via the drop-in API which
+is a thin ctypes layer over it).
+"""
+import ctypes
+import math
+
+import pytest
+import torch
+
+from co_alibi_attn import _native, co_alibi_attention
+from co_alibi_attn.workloads import WORKLOADS, make_inputs
+from oracle import co_alibi_ref as ref
+from tests.test_golden import GOLDEN, load_golden
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+TOL = {torch.float32: 1e-4, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+
+
+def hip_fwd_bwd(q, k, v, do, causal=True, sm_scale=None, bias_max=8.0):
+    """Drop-in API forward + backward on the GPU; returns CPU fp32 (o, dq, dk, dv)."""
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    o = co_alibi_attention(qd, kd, vd, causal=causal, sm_scale=sm_scale, bias_max=bias_max)
+    o.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    return tuple(t.detach().float().cpu() for t in (o, qd.grad, kd.grad, vd.grad))
+
+
+def oracle_fwd_bwd(q, k, v, do, causal=True, sm_scale=None, bias_max=8.0, heads=None):
+    lam = ref.slopes(q.shape[1], bias_max, dtype=q.dtype).float()
+    qf, kf, vf, dof = (t.float() for t in (q, k, v, do))
+    scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else sm_scale
+    o, lse = ref.forward(qf, kf, vf, lam, causal=causal, scale=scale, heads=heads)
+    dq, dk, dv = ref.backward(dof, qf, kf, vf, lam, causal=causal, scale=scale, heads=heads)
+    return o, lse, dq, dk, dv
+
+
+def rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=0, scale=0.5):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, Hq, Sq, D, generator=g) * scale).to(dtype)
+    k = (torch.randn(B, Hkv, Skv, D, generator=g) * scale).to(dtype)
+    v = (torch.randn(B, Hkv, Skv, D, generator=g) * scale).to(dtype)
+    do = torch.randn(B, Hq, Sq, D, generator=g).to(dtype)
+    return q, k, v, do
+
+
+def assert_parity(got, want, tol, label):
+    for name, g, w in zip(("o", "dq", "dk", "dv"), got, want):
+        assert torch.isfinite(g).all(), f"{label}: {name} has non-finite values"
+        err = (g - w.float()).abs().max().item()
+        print(f"  {label} {name}: max-abs {err:.3e} (tol {tol:g})", flush=True)
+        assert err <= tol, f"{label}: {name} max-abs {err:.3e} > {tol:g}"
+
+
+def hip_fwd_raw(q, k, v, slopes, causal, sm_scale):
+    """co_alibi_fwd through the C ABI; returns (o, lse, zb) on the device."""
+    lib = _native.lib()
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    o = torch.empty_like(q)
+    lse = torch.empty(B, Hq, Sq, device=DEV, dtype=torch.float32)
+    zb = torch.empty(lib.co_alibi_zb_numel(B, Hq, Sq, Skv), device=DEV, dtype=torch.float32)
+    _native.check(lib.co_alibi_fwd(_native.DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   slopes.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), B, Hq, Hkv,
+                                   Sq, Skv, D, int(causal), sm_scale, torch.cuda.current_stream().cuda_stream))
+    return o, lse, zb
+
+
+# --------------------------------------------------------------------------- small shapes
+
+def test_cpu_config_fp32_validation_mode():
+    """BASELINE configs[0] in the fp32 validation mode: max-abs <= 1e-4."""
+    w = WORKLOADS["cpu"]
+    q, k, v, do = make_inputs(w, seed=0)
+    got = hip_fwd_bwd(q, k, v, do, causal=True)
+    o, lse, dq, dk, dv = oracle_fwd_bwd(q, k, v, do, causal=True)
+    assert_parity(got, (o, dq, dk, dv), 1e-4, "cpu-config fp32")
+
+
+CASES = [
+    # (B, Hq, Hkv, Sq, Skv, D, causal)
+    (1, 2, 2, 128, 128, 64, True),
+    (1, 2, 2, 256, 256, 128, True),
+    (2, 4, 2, 200, 200, 64, True),      # tails, grouped heads
+    (1, 4, 1, 97, 97, 128, True),       # odd length, 4 query heads per key head
+    (1, 2, 2, 1, 1, 64, True),          # single query / key
+    (1, 2, 2, 1, 50, 128, True),        # Sq = 1 with many keys (only key 0 visible)
+    (1, 2, 2, 130, 77, 64, True),       # more queries than keys (top-left causal)
+    (1, 2, 2, 50, 300, 128, True),      # more keys than queries
+    (1, 2, 2, 100, 100, 64, False),     # non-causal
+    (1, 4, 2, 70, 190, 128, False),     # non-causal, rectangular, grouped
+    (1, 2, 2, 300, 300, 64, True),      # several key tiles, partial last tile
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "B{}H{}/{}S{}x{}D{}{}".format(*c[:6], "c" if c[6] else "n"))
+def test_small_shapes(case, dtype):
+    B, Hq, Hkv, Sq, Skv, D, causal = case
+    print(f"case {case} {dtype}", flush=True)
+    q, k, v, do = rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=1)
+    got = hip_fwd_bwd(q, k, v, do, causal=causal)
+    o, lse, dq, dk, dv = oracle_fwd_bwd(q, k, v, do, causal=causal)
+    assert_parity(got, (o, dq, dk, dv), TOL[dtype], f"{case}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
+def test_lse_and_penalty_statistics(dtype):
+    """LSE (natural log, m + log(l + 1e-9)) and zb (suffix sigmoid sums at 32-key block starts)."""
+    B, Hq, Hkv, S, D = 1, 2, 2, 150, 64
+    q, k, v, _ = rand_inputs(B, Hq, Hkv, S, S, D, dtype, seed=2)
+    lam = ref.slopes(Hq, dtype=dtype).float()
+    scale = 1.0 / math.sqrt(D)
+    o, lse, zb = hip_fwd_raw(q.to(DEV), k.to(DEV), v.to(DEV), lam.to(DEV), True, scale)
+    torch.cuda.synchronize()
+    _, lse_ref = ref.forward(q.float(), k.float(), v.float(), lam, causal=True, scale=scale)
+    tol = 1e-4 if dtype == torch.float32 else 5e-3
+    assert (lse.cpu() - lse_ref).abs().max().item() <= tol
+    nzb = (S + 31) // 32
+    zb = zb.view(B * Hq, nzb, S).cpu()
+    for h in range(Hq):
+        _, _, _, sig, _ = ref._rows_forward(q[0, h].float(), k[0, h].float(), v[0, h].float(), lam[h], True, scale, 0)
+        suffix = torch.cumsum(sig.flip(-1), -1).flip(-1)  # [i, j] = sum_{k >= j} sigma_ik
+        for J in range(nzb):
+            rows = torch.arange(32 * J, S)  # rows that see key 32*J
+            err = (zb[h, J, rows] - suffix[rows, 32 * J]).abs().max().item()
+            assert err <= 1e-3 * max(1.0, S / 32), f"zb head {h} block {J}: {err}"
+
+
+def test_split_backward_equals_full():
+    """co_alibi_bwd_dq then co_alibi_bwd_dkdv == co_alibi_bwd, bit for bit."""
+    lib = _native.lib()
+    B, Hq, Hkv, S, D = 1, 4, 2, 190, 128
+    dtype = torch.float16
+    q, k, v, do = (t.to(DEV) for t in rand_inputs(B, Hq, Hkv, S, S, D, dtype, seed=3))
+    lam = ref.slopes(Hq, dtype=dtype).float().to(DEV)
+    scale = 1.0 / math.sqrt(D)
+    o, lse, zb = hip_fwd_raw(q, k, v, lam, True, scale)
+    ws_bytes = lib.co_alibi_bwd_workspace_bytes(B, Hq, S, S)
+    st = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for split in (False, True):
+        ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        common = (B, Hq, Hkv, S, S, D, 1, scale, st)
+        if split:
+            _native.check(lib.co_alibi_bwd_dq(1, do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                              lse.data_ptr(), zb.data_ptr(), lam.data_ptr(), dq.data_ptr(),
+                                              ws.data_ptr(), ws_bytes, *common))
+            _native.check(lib.co_alibi_bwd_dkdv(1, do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                                lse.data_ptr(), zb.data_ptr(), lam.data_ptr(), dk.data_ptr(),
+                                                dv.data_ptr(), ws.data_ptr(), ws_bytes, *common))
+        else:
+            _native.check(lib.co_alibi_bwd(1, do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                           lse.data_ptr(), zb.data_ptr(), lam.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                                           dv.data_ptr(), ws.data_ptr(), ws_bytes, *common))
+        torch.cuda.synchronize()
+        outs.append((dq.cpu(), dk.cpu(), dv.cpu()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_repeat_call_deterministic():
+    q, k, v, do = rand_inputs(1, 4, 2, 333, 333, 128, torch.bfloat16, seed=4)
+    r1 = hip_fwd_bwd(q, k, v, do)
+    r2 = hip_fwd_bwd(q, k, v, do)
+    for a, b in zip(r1, r2):
+        assert torch.equal(a, b)
+
+
+def test_sm_scale_and_bias_max_arguments():
+    q, k, v, do = rand_inputs(1, 3, 3, 120, 120, 64, torch.float32, seed=5)
+    got = hip_fwd_bwd(q, k, v, do, causal=True, sm_scale=0.3, bias_max=4.0)
+    o, _, dq, dk, dv = oracle_fwd_bwd(q, k, v, do, causal=True, sm_scale=0.3, bias_max=4.0)
+    assert_parity(got, (o, dq, dk, dv), 1e-4, "sm_scale=0.3 bias_max=4 H=3")
+
+
+def test_unsupported_inputs_raise():
+    q = torch.randn(1, 2, 8, 96, device=DEV, dtype=torch.float16)
+    with pytest.raises(ValueError, match="head_dim"):
+        co_alibi_attention(q, q, q)
+    q = torch.randn(1, 2, 8, 64, device=DEV, dtype=torch.float64)
+    with pytest.raises(TypeError):
+        co_alibi_attention(q, q, q)
+
+
+# --------------------------------------------------------------------------- golden fixtures
+
+@pytest.mark.parametrize("path", GOLDEN, ids=lambda p: p.rsplit("/", 1)[-1][:-4])
+def test_golden_fixtures(path):
+    t, causal, sm_scale, bias_max, dtype_name = load_golden(path)
+    dtype = getattr(torch, dtype_name)
+    q, k, v, do = (t[n].to(dtype) for n in ("q", "k", "v", "do"))
+    got = hip_fwd_bwd(q, k, v, do, causal=causal, sm_scale=sm_scale, bias_max=bias_max)
+    assert_parity(got, (t["o"], t["dq"], t["dk"], t["dv"]), TOL[dtype], path.rsplit("/", 1)[-1])
+
+
+# --------------------------------------------------------------------------- full-size configs
+
+# Sampled (batch, query head) pairs checked against the oracle; dK/dV of a key
+# head are checked only where all its query heads are sampled.
+FULL = {
+    "headline": [(0, 0), (3, 15)],
+    "gqa": [(0, 4), (0, 5), (0, 6), (0, 7)],
+    "long": [(0, 0), (0, 7)],
+}
+
+
+@pytest.mark.parametrize("name", list(FULL))
+def test_full_size_config(name):
+    w = WORKLOADS[name]
+    print(f"config {name}: B{w.batch} Hq{w.heads_q} Hkv{w.heads_kv} S{w.seq} D{w.head_dim} {w.dtype}", flush=True)
+    q, k, v, do = make_inputs(w, seed=0)
+    o, dq, dk, dv = hip_fwd_bwd(q, k, v, do, causal=w.causal, bias_max=w.bias_max)
+    for name_, t in dict(o=o, dq=dq, dk=dk, dv=dv).items():
+        assert torch.isfinite(t).all(), f"{name_} not finite"
+    # Size-independent identity: sum over keys of dV = sum over rows of dO (weights sum to 1).
+    g = w.heads_q // w.heads_kv
+    dv_sum = dv.double().sum(2)                                             # (B, Hkv, D)
+    do_sum = do.double().view(w.batch, w.heads_kv, g, w.seq, w.head_dim).sum((2, 3))
+    rel = ((dv_sum - do_sum).abs().max() / do_sum.abs().max()).item()
+    print(f"  sum_j dV_j vs sum_i dO_i: rel {rel:.2e}", flush=True)
+    assert rel < 1e-2
+    heads = FULL[name]
+    ro, _, rdq, rdk, rdv = oracle_fwd_bwd(q, k, v, do, causal=w.causal, bias_max=w.bias_max, heads=heads)
+    for b, h in heads:
+        for n_, got, want in (("o", o, ro), ("dq", dq, rdq)):
+            err = (got[b, h] - want[b, h]).abs().max().item()
+            print(f"  {name} b{b} h{h} {n_}: max-abs {err:.3e}", flush=True)
+            assert err <= TOL[w.dtype]
+    kv_heads = {(b, h // g) for b, h in heads if all((b, hh) in heads for hh in range((h // g) * g, (h // g + 1) * g))}
+    for b, hk in sorted(kv_heads):
+        for n_, got, want in (("dk", dk, rdk), ("dv", dv, rdv)):
+            err = (got[b, hk] - want[b, hk]).abs().max().item()
+            print(f"  {name} b{b} kv{hk} {n_}: max-abs {err:.3e}", flush=True)
+            assert err <= TOL[w.dtype]
