@@ -17,11 +17,17 @@
 // need no atomics and no per-query-block partial buffers:
 //   pass 1 (query-major, keys left to right): S^T, dS^T, dP, dQ^T += K^T dP^T.
 //     It writes D_i and cb[i][J] = sum over keys k < 32J of dA_ik.
-//   pass 2 (key-major, one work-group per 128 keys of a key head): for every
-//     query head of the group and every query tile, S, dS, dP from the forward's
-//     zb and pass 1's cb, then dV^T += dO^T s and dK^T += Q^T dP.
-// z inside a 32-key block is zb[i][J] minus the exclusive prefix of sigma in
-// the block, so no long running sum is ever subtracted from.
+//   pass 2 (key-major, one work-group per 128 keys of a key head, 32 keys per
+//     wavefront): for every query head of the group and every query tile,
+//     S^T, dS^T, dP from the forward's zb and pass 1's cb, then
+//     dV^T += dO^T s and dK^T += Q^T dP.
+// Both passes hold keys on the accumulator rows (each lane: 16 consecutive keys
+// of one query), so both key scans stay in registers.  z inside a 32-key block
+// is zb[i][J] minus the exclusive prefix of sigma in the block, so no long
+// running sum is ever subtracted from.
+// Operands whose reduction runs over LDS rows (K^T in pass 1; Q^T, dO^T, s, dP
+// in pass 2) are read with ds_read_b64_tr_b16 from row-major tiles; the fp32
+// validation mode stores transposed copies instead.
 #include "coalibi_common.h"
 #include "coalibi_kernels.h"
 
@@ -29,142 +35,103 @@ namespace coalibi {
 
 namespace {
 
-constexpr int kBM = 128;  // pass 1: query rows per work-group
-constexpr int kBN = 64;   // pass 1: keys per tile
+constexpr int kBM = 128;  // pass 1: query rows per work-group (32 per wavefront)
+constexpr int kBN = 32;   // pass 1: keys per tile
 constexpr int kBK = 128;  // pass 2: keys per work-group (32 per wavefront)
-constexpr int kBQ = 64;   // pass 2: query rows per tile
+// pass 2: query rows per tile (32 in the fp32 validation mode, which also keeps
+// transposed copies of the tiles in LDS)
+template <typename T>
+constexpr int kBQ = sizeof(T) == 4 ? 32 : 64;
 
 template <typename T, int D>
 struct BwdCfg {
+  static constexpr bool kTr = sizeof(T) == 2;
   static constexpr int CH = 16 / sizeof(T);
-  static constexpr int LDR = D + CH;    // row-major tile stride (elements)
-  static constexpr int LDT = 64 + CH;   // transposed tile stride (64-row tiles)
+  static constexpr int LDR = D + 2 * CH;  // row-major tile stride (b128 row reads and transpose reads)
   static constexpr int KS = D / 16;
   static constexpr int DT = D / 32;
+  static constexpr int LDT1 = kBN + CH;   // fp32 pass 1: K^T tile stride
+  static constexpr int LDT2 = kBQ<T> + CH;  // fp32 pass 2: Q^T / dO^T tile stride
+  static constexpr int LDSP = kTr ? 32 + 2 * CH : 32 + CH;  // per-wave s / dP scratch stride
 };
 
-template <bool MASKED, bool CAUSAL>
-__device__ __forceinline__ bool pair_ok(int key, int row, int Skv, int Sq) {
-  if (!MASKED) return true;
-  return key < Skv && row < Sq && (!CAUSAL || key <= row);
+__device__ __forceinline__ bool pair_ok(int key, int row, int Skv, int Sq, bool causal) {
+  return key < Skv && row < Sq && (!causal || key <= row);
+}
+
+// Elementwise core shared by both passes for one 32-key x 32-query tile held as
+// S^T (lane (col, hh): query q, keys hh*16 + r).  Inputs: sacc = q.k, dacc = dO.v,
+// zb = sum of sigma over keys >= the block start, cb = sum of dA over keys before
+// the block, lse2 = LSE*log2(e), dsum = dO.O.  Outputs the 16 values of s and dP
+// packed for the next products; returns the block's dA total in `atot_blk`.
+template <typename T, bool MASKED, bool CAUSAL>
+__device__ __forceinline__ void dp_tile(const f32x16& sacc, f32x16& dacc, float zb, float cb, float lse2,
+                                        float dsum, int key0, int row, int hh, int Skv, int Sq, float sc2,
+                                        float lam, float lam2, typename Mfma<T>::vec8 (&sb)[2],
+                                        typename Mfma<T>::vec8 (&pb)[2], float& atot_blk) {
+  using M = Mfma<T>;
+  // Phase 1: sigma and this run's sigma total.
+  float sg[16];
+  float tot = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float s = sigmoid_log2(sacc[r] * sc2);
+    if (MASKED) s = pair_ok(key0 + r, row, Skv, Sq, CAUSAL) ? s : 0.f;
+    sg[r] = s;
+    tot += s;
+  }
+  // z = zb - (sigma of the other half's run if it is left of ours) - exclusive prefix.
+  const float oth = other_half(tot);
+  const float zbase = zb - (hh ? oth : 0.f);
+  // log2 of s:  t - lam2*(zbase - pre) - lse2 = fma(lam2, pre, fma(q.k, sc2, -(lam2*zbase + lse2)))
+  const float cst = fmaf(lam2, zbase, lse2);
+  float pre = 0.f, atot = 0.f;
+  f32x8 sv[2];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float s = fast_exp2(fmaf(lam2, pre, fmaf(sacc[r], sc2, -cst)));
+    pre += sg[r];
+    if (MASKED) s = pair_ok(key0 + r, row, Skv, Sq, CAUSAL) ? s : 0.f;
+    const float da = s * (dacc[r] - dsum);
+    dacc[r] = da;
+    atot += da;
+    sv[r >> 3][r & 7] = s;
+  }
+  sb[0] = M::pack(sv[0]);
+  sb[1] = M::pack(sv[1]);
+  // C = cb + (dA of the other half's run if left of ours) + inclusive prefix.
+  const float aoth = other_half(atot);
+  float c = cb + (hh ? aoth : 0.f);
+  atot_blk = hh ? atot + aoth : aoth + atot;  // same order in both halves
+#pragma unroll
+  for (int mh = 0; mh < 2; ++mh) {
+    f32x8 pv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int r = mh * 8 + e;
+      const float da = dacc[r];
+      c += da;
+      const float sgv = sg[r];
+      float dp = fmaf(-lam * fmaf(-sgv, sgv, sgv), c, da);
+      if (MASKED) dp = pair_ok(key0 + r, row, Skv, Sq, CAUSAL) ? dp : 0.f;
+      pv[e] = dp;
+    }
+    pb[mh] = M::pack(pv);
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1: dQ, D, cb.  Layout as in the forward: per wavefront 32 query rows,
-// register r of 32-key subtile st of lane (col, hh) <-> key k0 + st*32 + hh*16 + r.
-template <typename T, int D, bool CAUSAL, bool MASKED>
-__device__ __forceinline__ void dq_tile(const T* __restrict__ sK, const T* __restrict__ sV,
-                                        const T* __restrict__ sKt,
-                                        const typename Mfma<T>::vec8 (&qf)[BwdCfg<T, D>::KS],
-                                        const typename Mfma<T>::vec8 (&dof)[BwdCfg<T, D>::KS],
-                                        f32x16 (&acc)[BwdCfg<T, D>::DT], float& crun, float& cb0,
-                                        float& cb1, float zb0, float zb1, float lse2, float dsum,
-                                        int k0, int row, int col, int hh, int Skv, int Sq, float sc2,
-                                        float lam, float lam2) {
-  using C = BwdCfg<T, D>;
-  using M = Mfma<T>;
-
-  f32x16 sacc[2], dacc[2];
-#pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    sacc[st] = f32x16{};
-    dacc[st] = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-      sacc[st] = M::k16(ld_vec8(sK + (st * 32 + col) * C::LDR + ks * 16 + hh * 8), qf[ks], sacc[st]);
-      dacc[st] = M::k16(ld_vec8(sV + (st * 32 + col) * C::LDR + ks * 16 + hh * 8), dof[ks], dacc[st]);
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  float sg[2][16];
-  float tot[2];
-#pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    float sum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float tv = sacc[st][r] * sc2;
-      float s = sigmoid_log2(tv);
-      if (MASKED) s = pair_ok<MASKED, CAUSAL>(k0 + st * 32 + hh * 16 + r, row, Skv, Sq) ? s : 0.f;
-      sacc[st][r] = tv;
-      sg[st][r] = s;
-      sum += s;
-    }
-    tot[st] = sum;
-  }
-  // z = zb[block] - (exclusive prefix of sigma inside the 32-key block).
-  const float oth0 = other_half(tot[0]), oth1 = other_half(tot[1]);
-  const float zbase[2] = {zb0 - (hh ? oth0 : 0.f), zb1 - (hh ? oth1 : 0.f)};
-
-  float atot[2];
-#pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    float pre = 0.f, sum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float z = zbase[st] - pre;
-      pre += sg[st][r];
-      float s = fast_exp2(sacc[st][r] - lam2 * z - lse2);
-      if (MASKED) s = pair_ok<MASKED, CAUSAL>(k0 + st * 32 + hh * 16 + r, row, Skv, Sq) ? s : 0.f;
-      const float da = s * (dacc[st][r] - dsum);
-      dacc[st][r] = da;
-      sum += da;
-    }
-    atot[st] = sum;
-  }
-  // Inclusive prefix of dA over keys, carried across blocks in crun.
-  const float ao0 = other_half(atot[0]), ao1 = other_half(atot[1]);
-  const float A00 = hh ? ao0 : atot[0], A01 = hh ? atot[0] : ao0;
-  const float A10 = hh ? ao1 : atot[1], A11 = hh ? atot[1] : ao1;
-  cb0 = crun;
-  cb1 = (cb0 + A00) + A01;
-  crun = (cb1 + A10) + A11;
-  const float cbase[2] = {cb0 + (hh ? A00 : 0.f), cb1 + (hh ? A10 : 0.f)};
-
-  typename M::vec8 pb[2][2];
-#pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    float c = cbase[st];
-#pragma unroll
-    for (int mh = 0; mh < 2; ++mh) {
-      f32x8 pv;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int r = mh * 8 + e;
-        const float da = dacc[st][r];
-        c += da;
-        const float sgv = sg[st][r];
-        float dp = da - lam * (sgv - sgv * sgv) * c;
-        if (MASKED) dp = pair_ok<MASKED, CAUSAL>(k0 + st * 32 + hh * 16 + r, row, Skv, Sq) ? dp : 0.f;
-        pv[e] = dp;
-      }
-      pb[st][mh] = M::pack(pv);
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  // dQ^T[d][q] += K^T[d][key] dP^T[key][q]
-#pragma unroll
-  for (int dt = 0; dt < C::DT; ++dt) {
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-#pragma unroll
-      for (int mh = 0; mh < 2; ++mh)
-        acc[dt] = M::k16(ld_vec8(sKt + (dt * 32 + col) * C::LDT + st * 32 + hh * 16 + mh * 8),
-                         pb[st][mh], acc[dt]);
-    }
-  }
-}
-
+// Pass 1: dQ, D, cb.  Per wavefront 32 query rows; register r of lane (col, hh)
+// <-> key k0 + hh*16 + r.
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void coalibi_bwd_dq_kernel(BwdArgs args) {
+__global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_bwd_dq_kernel(BwdArgs args) {
   using C = BwdCfg<T, D>;
   using M = Mfma<T>;
   using vec8 = typename M::vec8;
-  using Tile = TileLoader<T, D, kBN>;
+  using Tile = TileLoader<T, D, kBN, !BwdCfg<T, D>::kTr>;
   __shared__ __align__(16) T sK[kBN * C::LDR];
   __shared__ __align__(16) T sV[kBN * C::LDR];
-  __shared__ __align__(16) T sKt[D * C::LDT];
+  __shared__ __align__(16) T sKt[C::kTr ? 8 : D * C::LDT1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, hh = lane >> 5;
@@ -224,8 +191,8 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dq_kernel(BwdArgs args) {
   for (int kt = 0; kt < nkt; ++kt) {
     __syncthreads();
     kregs.store_rows(sK, C::LDR, tid);
-    kregs.store_cols(sKt, C::LDT, tid);
     vregs.store_rows(sV, C::LDR, tid);
+    if constexpr (!C::kTr) kregs.store_cols(sKt, C::LDT1, tid);
     __syncthreads();
     if (kt + 1 < nkt) {
       kregs.load(Kp, (kt + 1) * kBN, Skv, tid);
@@ -233,20 +200,39 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dq_kernel(BwdArgs args) {
     }
     const int k0 = kt * kBN;
     if (CAUSAL && k0 > wrow0 + 31) continue;  // every key of the tile is above this wavefront's rows
-    const bool has2 = k0 + 32 < Skv;          // second 32-key block exists
-    const float zb0 = row_ok ? zb_row[(size_t)(2 * kt) * Sq] : 0.f;
-    const float zb1 = (row_ok && has2) ? zb_row[(size_t)(2 * kt + 1) * Sq] : 0.f;
+    const float zb = row_ok ? zb_row[(size_t)kt * Sq] : 0.f;
     const bool masked = (CAUSAL && k0 + kBN - 1 > wrow0) || (k0 + kBN > Skv) || (wrow0 + 32 > Sq);
-    float cb0, cb1;
+
+    f32x16 sacc = f32x16{}, dacc = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
+      sacc = M::k16(ld_vec8(sK + col * C::LDR + ks * 16 + hh * 8), qf[ks], sacc);
+      dacc = M::k16(ld_vec8(sV + col * C::LDR + ks * 16 + hh * 8), dof[ks], dacc);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    vec8 sb[2], pb[2];
+    float atot;
     if (masked)
-      dq_tile<T, D, CAUSAL, true>(sK, sV, sKt, qf, dof, acc, crun, cb0, cb1, zb0, zb1, lse2, dsum, k0,
-                                  row, col, hh, Skv, Sq, args.sc2, lam, lam2);
+      dp_tile<T, true, CAUSAL>(sacc, dacc, zb, crun, lse2, dsum, k0 + hh * 16, row, hh, Skv, Sq, args.sc2, lam,
+                               lam2, sb, pb, atot);
     else
-      dq_tile<T, D, CAUSAL, false>(sK, sV, sKt, qf, dof, acc, crun, cb0, cb1, zb0, zb1, lse2, dsum, k0,
-                                   row, col, hh, Skv, Sq, args.sc2, lam, lam2);
-    if (hh == 0 && row_ok) {
-      cb_row[(size_t)(2 * kt) * Sq] = cb0;
-      if (has2) cb_row[(size_t)(2 * kt + 1) * Sq] = cb1;
+      dp_tile<T, false, CAUSAL>(sacc, dacc, zb, crun, lse2, dsum, k0 + hh * 16, row, hh, Skv, Sq, args.sc2,
+                                lam, lam2, sb, pb, atot);
+    if (hh == 0 && row_ok) cb_row[(size_t)kt * Sq] = crun;
+    crun += atot;
+    __builtin_amdgcn_sched_barrier(0);
+    // dQ^T[d][q] += K^T[d][key] dP^T[key][q];  A rows are keys hh*16 + mh*8 + e.
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh) {
+        vec8 ka;
+        if constexpr (C::kTr)
+          ka = ld_kmajor<T, true>(sK, C::LDR, mh * 8, 16, dt * 32, lane);
+        else
+          ka = ld_vec8(sKt + (dt * 32 + col) * C::LDT1 + hh * 16 + mh * 8);
+        acc[dt] = M::k16(ka, pb[mh], acc[dt]);
+      }
     }
   }
 
@@ -267,86 +253,25 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dq_kernel(BwdArgs args) {
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2: dK, dV.  Per wavefront 32 keys (lanes, col = key); accumulator rows
-// are queries: register r of query subtile sq of lane (col, hh) <-> query row
-// q0 + sq*32 + hh*16 + r.  Key-axis scans run across the 32 lanes of a half.
-template <typename T, int D, bool CAUSAL, bool MASKED>
-__device__ __forceinline__ void dkdv_tile(const T* __restrict__ sQ, const T* __restrict__ sdO,
-                                          const T* __restrict__ sQt, const T* __restrict__ sdOt,
-                                          const float* __restrict__ sLse2,
-                                          const float* __restrict__ sDsum,
-                                          const float* __restrict__ sZb, const float* __restrict__ sCb,
-                                          const typename Mfma<T>::vec8 (&kf)[BwdCfg<T, D>::KS],
-                                          const typename Mfma<T>::vec8 (&vf)[BwdCfg<T, D>::KS],
-                                          f32x16 (&dk)[BwdCfg<T, D>::DT],
-                                          f32x16 (&dv)[BwdCfg<T, D>::DT], int sq, int qs0, int key,
-                                          int col, int hh, int Skv, int Sq, float sc2, float lam,
-                                          float lam2) {
-  using C = BwdCfg<T, D>;
-  using M = Mfma<T>;
-
-  f32x16 sacc = f32x16{}, dacc = f32x16{};
-#pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) {
-    sacc = M::k16(ld_vec8(sQ + (sq * 32 + col) * C::LDR + ks * 16 + hh * 8), kf[ks], sacc);
-    dacc = M::k16(ld_vec8(sdO + (sq * 32 + col) * C::LDR + ks * 16 + hh * 8), vf[ks], dacc);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  const int ql0 = sq * 32 + hh * 16;  // tile-local query of register 0
-  typename M::vec8 sb[2], pb[2];
-#pragma unroll
-  for (int mh = 0; mh < 2; ++mh) {
-    f32x8 sv, pv;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int r = mh * 8 + e;
-      const int ql = ql0 + r;
-      const bool ok = pair_ok<MASKED, CAUSAL>(key, qs0 + hh * 16 + r, Skv, Sq);
-      const float tv = sacc[r] * sc2;
-      float sg = sigmoid_log2(tv);
-      if (MASKED) sg = ok ? sg : 0.f;
-      const float pin = half_wave_prefix(sg);
-      const float z = sZb[ql] - pin + sg;
-      float s = fast_exp2(tv - lam2 * z - sLse2[ql]);
-      if (MASKED) s = ok ? s : 0.f;
-      const float da = s * (dacc[r] - sDsum[ql]);
-      const float c = sCb[ql] + half_wave_prefix(da);
-      float dp = da - lam * (sg - sg * sg) * c;
-      if (MASKED) dp = ok ? dp : 0.f;
-      sv[e] = s;
-      pv[e] = dp;
-    }
-    sb[mh] = M::pack(sv);
-    pb[mh] = M::pack(pv);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  // dV^T[d][key] += dO^T[d][q] s[q][key];  dK^T[d][key] += Q^T[d][q] dP[q][key]
-#pragma unroll
-  for (int dt = 0; dt < C::DT; ++dt) {
-#pragma unroll
-    for (int mh = 0; mh < 2; ++mh) {
-      const int off = (dt * 32 + col) * C::LDT + sq * 32 + hh * 16 + mh * 8;
-      dv[dt] = M::k16(ld_vec8(sdOt + off), sb[mh], dv[dt]);
-      dk[dt] = M::k16(ld_vec8(sQt + off), pb[mh], dk[dt]);
-    }
-  }
-}
-
+// Pass 2: dK, dV.  Per wavefront the 32 keys kw0.. of one 32-key block, held as
+// MFMA A operands (row R <-> key kw0 + kRowOfReg(R)) so that register r of lane
+// (col, hh) of S^T <-> key kw0 + hh*16 + r, query q0 + sq*32 + col.
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_kernel(BwdArgs args) {
   using C = BwdCfg<T, D>;
   using M = Mfma<T>;
   using vec8 = typename M::vec8;
-  using Tile = TileLoader<T, D, kBQ>;
-  __shared__ __align__(16) T sQ[kBQ * C::LDR];
-  __shared__ __align__(16) T sdO[kBQ * C::LDR];
-  __shared__ __align__(16) T sQt[D * C::LDT];
-  __shared__ __align__(16) T sdOt[D * C::LDT];
-  __shared__ __align__(16) float sLse2[kBQ];
-  __shared__ __align__(16) float sDsum[kBQ];
-  __shared__ __align__(16) float sZb[4][kBQ];
-  __shared__ __align__(16) float sCb[4][kBQ];
+  constexpr int BQ = kBQ<T>;
+  using Tile = TileLoader<T, D, BQ, !BwdCfg<T, D>::kTr>;
+  __shared__ __align__(16) T sQ[BQ * C::LDR];
+  __shared__ __align__(16) T sdO[BQ * C::LDR];
+  __shared__ __align__(16) T sQt[C::kTr ? 8 : D * C::LDT2];
+  __shared__ __align__(16) T sdOt[C::kTr ? 8 : D * C::LDT2];
+  __shared__ __align__(16) T sSP[4][2][32 * C::LDSP];  // per wavefront: s and dP, [q][key] (fp32: [key][q])
+  __shared__ __align__(16) float sLse2[BQ];
+  __shared__ __align__(16) float sDsum[BQ];
+  __shared__ __align__(16) float sZb[4][BQ];
+  __shared__ __align__(16) float sCb[4][BQ];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, hh = lane >> 5;
@@ -359,17 +284,21 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_kernel(BwdArgs args) 
   const int group = args.Hq / args.Hkv;
   const size_t kvoff = (size_t)bhk * Skv * D;
   const int kw0 = kb * kBK + wave * 32;    // first key of this wavefront
-  const int key = kw0 + col;
+  const int jblk = kw0 / 32;               // its 32-key block
+  const int key0 = kw0 + hh * 16;          // key of register 0 of this lane
+  T* __restrict__ sS = sSP[wave][0];
+  T* __restrict__ sP = sSP[wave][1];
 
-  vec8 kf[C::KS], vf[C::KS];
+  vec8 ka[C::KS], va[C::KS];
   {
+    const int key = kw0 + kRowOfReg(col);
     const bool key_ok = key < Skv;
     const T* __restrict__ Kr = static_cast<const T*>(args.k) + kvoff + (size_t)key * D;
     const T* __restrict__ Vr = static_cast<const T*>(args.v) + kvoff + (size_t)key * D;
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
-      kf[ks] = key_ok ? ld_vec8(Kr + ks * 16 + hh * 8) : zero_vec8<T>();
-      vf[ks] = key_ok ? ld_vec8(Vr + ks * 16 + hh * 8) : zero_vec8<T>();
+      ka[ks] = key_ok ? ld_vec8(Kr + ks * 16 + hh * 8) : zero_vec8<T>();
+      va[ks] = key_ok ? ld_vec8(Vr + ks * 16 + hh * 8) : zero_vec8<T>();
     }
   }
 
@@ -380,65 +309,123 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_kernel(BwdArgs args) 
     dv[dt] = f32x16{};
   }
 
-  const int nQT = (Sq + kBQ - 1) / kBQ;
-  const int qt0 = CAUSAL ? (kb * kBK) / kBQ : 0;
+  // Work list: (query head gi, query tile qt) pairs, prefetched one ahead.
+  const int nQT = (Sq + BQ - 1) / BQ;
+  const int qt0 = CAUSAL ? min((kb * kBK) / BQ, nQT) : 0;
+  const int per_head = nQT - qt0;
+  const int nwork = per_head * group;
   Tile qregs, doregs;
-  for (int gi = 0; gi < group; ++gi) {
+  float st_lse = 0.f, st_dsum = 0.f, st_zb = 0.f, st_cb = 0.f;  // per-row statistics for the next tile
+  auto prefetch = [&](int w) {
+    const int gi = w / per_head, qt = qt0 + (w - gi * per_head);
+    const int bh = b * args.Hq + hkv * group + gi;
+    const size_t qoff = (size_t)bh * Sq * D;
+    const int q0 = qt * BQ;
+    qregs.load(static_cast<const T*>(args.q) + qoff, q0, Sq, tid);
+    doregs.load(static_cast<const T*>(args.dout) + qoff, q0, Sq, tid);
+    const int q = q0 + lane;
+    const bool ok = lane < BQ && q < Sq;
+    const int jb = kb * (kBK / 32) + wave;  // the 32-key block of wavefront `wave`
+    const bool jok = ok && jb < args.nZB;
+    st_lse = ok ? args.lse[(size_t)bh * Sq + q] * kLog2e : 0.f;
+    st_dsum = ok ? args.dsum[(size_t)bh * Sq + q] : 0.f;
+    st_zb = jok ? args.zb[((size_t)bh * args.nZB + jb) * Sq + q] : 0.f;
+    st_cb = jok ? args.cb[((size_t)bh * args.nZB + jb) * Sq + q] : 0.f;
+  };
+  if (nwork > 0) prefetch(0);
+
+  for (int w = 0; w < nwork; ++w) {
+    const int gi = w / per_head, qt = qt0 + (w - gi * per_head);
     const int hq = hkv * group + gi;
-    const int bh = b * args.Hq + hq;
     const float lam = args.slopes[hq];
     const float lam2 = lam * kLog2e;
-    const size_t qoff = (size_t)bh * Sq * D;
-    const T* __restrict__ Qp = static_cast<const T*>(args.q) + qoff;
-    const T* __restrict__ dOp = static_cast<const T*>(args.dout) + qoff;
-    const float* __restrict__ lse = args.lse + (size_t)bh * Sq;
-    const float* __restrict__ dsum = args.dsum + (size_t)bh * Sq;
-    const float* __restrict__ zb = args.zb + (size_t)bh * args.nZB * Sq;
-    const float* __restrict__ cb = args.cb + (size_t)bh * args.nZB * Sq;
-    for (int qt = qt0; qt < nQT; ++qt) {
-      const int q0 = qt * kBQ;
-      qregs.load(Qp, q0, Sq, tid);
-      doregs.load(dOp, q0, Sq, tid);
-      __syncthreads();
-      qregs.store_rows(sQ, C::LDR, tid);
-      qregs.store_cols(sQt, C::LDT, tid);
-      doregs.store_rows(sdO, C::LDR, tid);
-      doregs.store_cols(sdOt, C::LDT, tid);
-      {
-        // Per-row statistics: tid < 64 -> lse and D, 64..255 -> zb / cb of the wavefronts.
-        const int rl = tid & 63;
-        const int q = q0 + rl;
-        const bool ok = q < Sq;
-        if (tid < 64) {
-          sLse2[rl] = ok ? lse[q] * kLog2e : 0.f;
-          sDsum[rl] = ok ? dsum[q] : 0.f;
-        }
-        const int w = tid >> 6;  // zb/cb for wavefront w (its 32-key block)
-        const int jb = kb * (kBK / 32) + w;
-        const bool jok = ok && jb < args.nZB;
-        sZb[w][rl] = jok ? zb[(size_t)jb * Sq + q] : 0.f;
-        sCb[w][rl] = jok ? cb[(size_t)jb * Sq + q] : 0.f;
+    const int q0 = qt * BQ;
+    __syncthreads();
+    qregs.template store_rows<false>(sQ, C::LDR, tid);
+    doregs.template store_rows<false>(sdO, C::LDR, tid);
+    if constexpr (!C::kTr) {
+      qregs.store_cols(sQt, C::LDT2, tid);
+      doregs.store_cols(sdOt, C::LDT2, tid);
+    }
+    if (lane < BQ) {
+      if (wave == 0) {
+        sLse2[lane] = st_lse;
+        sDsum[lane] = st_dsum;
       }
-      __syncthreads();
-      if (kw0 < Skv) {
+      sZb[wave][lane] = st_zb;
+      sCb[wave][lane] = st_cb;
+    }
+    __syncthreads();
+    if (w + 1 < nwork) prefetch(w + 1);
+    if (kw0 >= Skv) continue;
 #pragma unroll
-        for (int sq = 0; sq < 2; ++sq) {
-          const int qs0 = q0 + sq * 32;
-          if (CAUSAL && qs0 + 31 < kw0) continue;  // every row of the subtile precedes the keys
-          const bool masked = (CAUSAL && qs0 < kw0 + 31) || (qs0 + 32 > Sq) || (kw0 + 32 > Skv);
-          if (masked)
-            dkdv_tile<T, D, CAUSAL, true>(sQ, sdO, sQt, sdOt, sLse2, sDsum, sZb[wave], sCb[wave], kf, vf,
-                                          dk, dv, sq, qs0, key, col, hh, Skv, Sq, args.sc2, lam, lam2);
-          else
-            dkdv_tile<T, D, CAUSAL, false>(sQ, sdO, sQt, sdOt, sLse2, sDsum, sZb[wave], sCb[wave], kf,
-                                           vf, dk, dv, sq, qs0, key, col, hh, Skv, Sq, args.sc2, lam,
-                                           lam2);
+    for (int sq = 0; sq < BQ / 32; ++sq) {
+      const int qs0 = q0 + sq * 32;
+      if (CAUSAL && qs0 + 31 < kw0) continue;  // every row of the subtile precedes the keys
+      const bool masked = (CAUSAL && qs0 < kw0 + 31) || (qs0 + 32 > Sq) || (kw0 + 32 > Skv);
+      const int ql = sq * 32 + col;  // tile-local query row of this lane
+      const int row = qs0 + col;
+
+      f32x16 sacc = f32x16{}, dacc = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks) {
+        sacc = M::k16(ka[ks], ld_vec8(sQ + ql * C::LDR + ks * 16 + hh * 8), sacc);
+        dacc = M::k16(va[ks], ld_vec8(sdO + ql * C::LDR + ks * 16 + hh * 8), dacc);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      vec8 sb[2], pb[2];
+      float atot;
+      if (masked)
+        dp_tile<T, true, CAUSAL>(sacc, dacc, sZb[wave][ql], sCb[wave][ql], sLse2[ql], sDsum[ql], key0, row, hh,
+                                 Skv, Sq, args.sc2, lam, lam2, sb, pb, atot);
+      else
+        dp_tile<T, false, CAUSAL>(sacc, dacc, sZb[wave][ql], sCb[wave][ql], sLse2[ql], sDsum[ql], key0, row, hh,
+                                  Skv, Sq, args.sc2, lam, lam2, sb, pb, atot);
+      // s and dP to this wavefront's scratch, then back as operands reduced over queries.
+      if constexpr (C::kTr) {
+        *reinterpret_cast<vec8*>(sS + col * C::LDSP + hh * 16) = sb[0];
+        *reinterpret_cast<vec8*>(sS + col * C::LDSP + hh * 16 + 8) = sb[1];
+        *reinterpret_cast<vec8*>(sP + col * C::LDSP + hh * 16) = pb[0];
+        *reinterpret_cast<vec8*>(sP + col * C::LDSP + hh * 16 + 8) = pb[1];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sS[(hh * 16 + r) * C::LDSP + col] = sb[r >> 3][r & 7];
+          sP[(hh * 16 + r) * C::LDSP + col] = pb[r >> 3][r & 7];
         }
       }
-      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      // dV^T[d][key] += dO^T[d][q] s[q][key];  dK^T[d][key] += Q^T[d][q] dP[q][key]
+      // reduction rows (queries) mh*16 + kh*8 + e of the subtile.
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh) {
+        vec8 sop, pop;
+        if constexpr (C::kTr) {
+          sop = ld_kmajor<T, false>(sS, C::LDSP, mh * 16, 8, 0, lane);
+          pop = ld_kmajor<T, false>(sP, C::LDSP, mh * 16, 8, 0, lane);
+        } else {
+          sop = ld_vec8(sS + col * C::LDSP + mh * 16 + hh * 8);
+          pop = ld_vec8(sP + col * C::LDSP + mh * 16 + hh * 8);
+        }
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+          vec8 doa, qa;
+          if constexpr (C::kTr) {
+            doa = ld_kmajor<T, false>(sdO, C::LDR, sq * 32 + mh * 16, 8, dt * 32, lane);
+            qa = ld_kmajor<T, false>(sQ, C::LDR, sq * 32 + mh * 16, 8, dt * 32, lane);
+          } else {
+            doa = ld_vec8(sdOt + (dt * 32 + col) * C::LDT2 + sq * 32 + mh * 16 + hh * 8);
+            qa = ld_vec8(sQt + (dt * 32 + col) * C::LDT2 + sq * 32 + mh * 16 + hh * 8);
+          }
+          dv[dt] = M::k16(doa, sop, dv[dt]);
+          dk[dt] = M::k16(qa, pop, dk[dt]);
+        }
+      }
     }
   }
+  (void)jblk;
 
+  const int key = kw0 + col;
   if (key < Skv) {
     using vec4 = typename VecOf<T, 4>::type;
     T* __restrict__ dKr = static_cast<T*>(args.dk) + kvoff + (size_t)key * D;
@@ -479,7 +466,7 @@ hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream) {
   return hipSuccess;
 }
 
-#define COALIBI_INST_BWD(T, D)                                           \
+#define COALIBI_INST_BWD(T, D)                                                \
   template hipError_t launch_bwd<T, D, true>(const BwdArgs&, int, hipStream_t); \
   template hipError_t launch_bwd<T, D, false>(const BwdArgs&, int, hipStream_t);
 

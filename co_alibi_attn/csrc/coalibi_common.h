@@ -124,25 +124,31 @@ namespace coalibi {
 template <typename T, int N> struct VecOf { typedef T type __attribute__((ext_vector_type(N))); };
 
 // Stages a ROWS x D tile of a row-major [rows][D] matrix through registers into
-// LDS.  Each thread owns KG consecutive rows x one 16-byte column chunk, so the
-// same registers can be written both row-major (store_rows: rows permuted with
-// kRegOfRow inside every 32-row block, the layout the A operand of a
-// "rows along registers" product reads) and transposed (store_cols: the
-// [D][rows] layout the A operand of a "reduce over rows" product reads).
-// Rows at or beyond `nrows` read as zero.
-template <typename T, int D, int ROWS>
+// LDS, 16 bytes per load/store.  Rows at or beyond `nrows` read as zero.
+//   GROUPED = false: consecutive threads own consecutive 16-byte chunks of a row
+//     (coalesced loads, conflict-free row stores); only store_rows is available.
+//   GROUPED = true: each thread owns KG consecutive rows x one chunk, so the same
+//     registers can also be written transposed (store_cols, the [D][rows] layout
+//     used where no transpose read exists, i.e. for fp32).
+// store_rows<PERM> writes row-major; with PERM, rows are permuted with kRegOfRow
+// inside every 32-row block (the layout the A operand of a "rows along
+// registers" product reads in lane order).
+template <typename T, int D, int ROWS, bool GROUPED = false>
 struct TileLoader {
-  static constexpr int CH = 16 / sizeof(T);                       // elements per chunk
-  static constexpr int KG = ((ROWS / 4) * (D / CH) >= 256) ? 4 : 2;  // rows per thread group
-  static constexpr int NG = (ROWS / KG) * (D / CH);                // groups per tile
-  static constexpr int GPT = NG / 256;                             // groups per thread
+  static constexpr int CH = 16 / sizeof(T);  // elements per chunk
+  static constexpr int CPR = D / CH;         // chunks per row
+  // Rows per thread group: the largest of 4, 2, 1 that still gives every thread a group.
+  static constexpr int KG = !GROUPED ? 1
+                            : ((ROWS / 4) * CPR >= 256) ? 4 : ((ROWS / 2) * CPR >= 256) ? 2 : 1;
+  static constexpr int NG = (ROWS / KG) * CPR;  // groups per tile
+  static constexpr int GPT = NG / 256;          // groups per thread
   static_assert(NG % 256 == 0 && GPT >= 1, "tile does not split over 256 threads");
   static_assert(ROWS % 32 == 0, "rows are permuted in blocks of 32");
 
   u32x4 r[GPT][KG];
 
-  __device__ __forceinline__ static int grp_row(int g) { return (g % (ROWS / KG)) * KG; }
-  __device__ __forceinline__ static int grp_col(int g) { return (g / (ROWS / KG)) * CH; }
+  __device__ __forceinline__ static int grp_row(int g) { return GROUPED ? (g % (ROWS / KG)) * KG : g / CPR; }
+  __device__ __forceinline__ static int grp_col(int g) { return GROUPED ? (g / (ROWS / KG)) * CH : (g % CPR) * CH; }
 
   __device__ __forceinline__ void load(const T* __restrict__ base, int row0, int nrows, int tid) {
 #pragma unroll
@@ -157,7 +163,7 @@ struct TileLoader {
     }
   }
 
-  // s[R * ld + c] with R = (row & ~31) | kRegOfRow(row & 31)
+  template <bool PERM = true>
   __device__ __forceinline__ void store_rows(T* s, int ld, int tid) const {
 #pragma unroll
     for (int i = 0; i < GPT; ++i) {
@@ -166,7 +172,7 @@ struct TileLoader {
 #pragma unroll
       for (int k = 0; k < KG; ++k) {
         const int row = rr + k;
-        const int R = (row & ~31) | kRegOfRow(row & 31);
+        const int R = PERM ? ((row & ~31) | kRegOfRow(row & 31)) : row;
         st16(s + R * ld + cc, r[i][k]);
       }
     }
@@ -174,6 +180,7 @@ struct TileLoader {
 
   // s[c * ld + row] (rows in natural order)
   __device__ __forceinline__ void store_cols(T* s, int ld, int tid) const {
+    static_assert(GROUPED, "store_cols needs the grouped layout");
     using chunk = typename VecOf<T, CH>::type;
     using grp = typename VecOf<T, KG>::type;
 #pragma unroll
@@ -193,5 +200,66 @@ struct TileLoader {
     }
   }
 };
+
+}  // namespace coalibi
+
+namespace coalibi {
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __fp16 tr_f16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __bf16 tr_bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
+
+// Physical LDS row of logical row r in a tile stored with store_rows<true>.
+__device__ __forceinline__ int perm_row(int r) { return (r & ~31) | kRegOfRow(r & 31); }
+
+// One ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives
+// element j of the 8 bytes addressed by group-lane 4*j + i/4, position i%4.
+template <typename T>
+__device__ __forceinline__ u32x2 lds_tr4(const T* p) {
+  if constexpr (__is_same(T, _Float16)) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                         (__attribute__((address_space(3))) tr_f16x4*)(p)));
+  } else {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                                         (__attribute__((address_space(3))) tr_bf16x4*)(p)));
+  }
+}
+
+// MFMA 32x32x16 operand whose reduction index runs along the rows of a
+// row-major 16-bit LDS tile: lane l receives tile[row(l/32, e)][col0 + l%32]
+// for e = 0..7, with row(kh, e) = rbase + kh*khs + e (through perm_row when
+// PERM).  Two transpose reads; each 16-lane group gathers 4 rows x 16 columns.
+template <typename T, bool PERM>
+__device__ __forceinline__ typename Mfma<T>::vec8 ld_kmajor(const T* tile, int ld, int rbase, int khs,
+                                                              int col0, int lane) {
+  static_assert(sizeof(T) == 2, "transpose reads are 16-bit only");
+  const int i = lane & 15, g = lane >> 4;
+  const int col = col0 + 16 * (g & 1) + 4 * (i & 3);
+  const int r0 = rbase + (g >> 1) * khs + (i >> 2);
+  const int ra = PERM ? perm_row(r0) : r0;
+  const int rb = PERM ? perm_row(r0 + 4) : r0 + 4;
+  const u32x2 lo = lds_tr4(tile + ra * ld + col);
+  const u32x2 hi = lds_tr4(tile + rb * ld + col);
+  return __builtin_bit_cast(typename Mfma<T>::vec8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+}
+
+// Adds the eight values of a packed operand to an fp32 sum.
+__device__ __forceinline__ float sum8(f16x8 v, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2(h2{v[e], v[e + 1]}, h2{1, 1}, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float sum8(bf16x8 v, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2_f32_bf16(b2{v[e], v[e + 1]}, b2{1, 1}, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float sum8(f32x8 v, float acc) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc += v[e];
+  return acc;
+}
 
 }  // namespace coalibi

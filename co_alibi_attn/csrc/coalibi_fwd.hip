@@ -17,7 +17,8 @@
 //   sigmoid, suffix scan (in registers + one exchange with the other half),
 //   penalty, online softmax (exp2, lazily rescaled), then
 //   O^T += V^T P^T (MFMA, the P accumulators are reused as the B operand).
-// K is staged in LDS row-major (rows permuted), V transposed ([d][key]).
+// K is staged in LDS row-major (rows permuted); V row-major, read as the
+// transposed operand with ds_read_b64_tr_b16 (fp32 mode: V stored transposed).
 // Besides O and LSE the kernel writes zb: the suffix sum at every 32-key block
 // start, the only penalty statistic the backward needs.
 #include "coalibi_common.h"
@@ -35,9 +36,13 @@ constexpr float kRescaleThreshold = 8.0f;
 
 template <typename T, int D>
 struct FwdCfg {
+  static constexpr bool kTr = sizeof(T) == 2;  // V through LDS transpose reads
   static constexpr int CH = 16 / sizeof(T);
   static constexpr int LDK = D + CH;       // sK row stride (elements)
-  static constexpr int LDV = kFwdBN + CH;  // sVt row stride
+  // sV: row-major [key][d] (stride keeps each 4-row transpose read on distinct
+  // banks) or, in fp32 mode, transposed [d][key].
+  static constexpr int LDV = kTr ? D + 2 * CH : kFwdBN + CH;
+  static constexpr int V_ELEMS = kTr ? kFwdBN * LDV : D * LDV;
   static constexpr int KS = D / 16;        // k16 steps over the head dim
   static constexpr int DT = D / 32;        // 32-row tiles of O^T
 };
@@ -48,14 +53,18 @@ __device__ __forceinline__ bool key_ok(int key, int row, int Skv) {
   return key < Skv && (!CAUSAL || key <= row);
 }
 
+// One 64-key tile for one wavefront.  State: acc (O^T, scaled by 2^-m2), m2
+// (log2-domain scale, -inf before the first visible key), lsum (this half's
+// share of sum_j 2^(a_j - m2)), zr (sigmoid sum of all keys right of the tile).
 template <typename T, int D, bool CAUSAL, bool MASKED>
-__device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __restrict__ sVt,
+__device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __restrict__ sV,
                                          const typename Mfma<T>::vec8 (&qf)[FwdCfg<T, D>::KS],
-                                         f32x16 (&acc)[FwdCfg<T, D>::DT], float& m2, float& mtrue,
-                                         float& lsum, float& zr, float& zst0, float& zst1, int k0,
-                                         int row, int col, int hh, int Skv, float sc2, float lam2) {
+                                         f32x16 (&acc)[FwdCfg<T, D>::DT], float& m2, float& lsum,
+                                         float& zr, float& zst0, float& zst1, int k0, int row, int lane,
+                                         int Skv, float sc2, float lam2) {
   using C = FwdCfg<T, D>;
   using M = Mfma<T>;
+  const int col = lane & 31, hh = lane >> 5;
 
   // S^T tile: two 32-key subtiles; register r of subtile st <-> key k0 + st*32 + hh*16 + r.
   f32x16 sacc[2];
@@ -66,24 +75,22 @@ __device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __re
     for (int ks = 0; ks < C::KS; ++ks)
       sacc[st] = M::k16(ld_vec8(sK + (st * 32 + col) * C::LDK + ks * 16 + hh * 8), qf[ks], sacc[st]);
   }
-
   __builtin_amdgcn_sched_barrier(0);
-  // In place: sacc becomes t = p*log2(e), then the log2-domain logit a.
-  float sg[2][16];
+
+  // sigma and its inclusive suffix sum inside each lane's 16-key run.
+  float loc[2][16];
   float tot[2];
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
-    float sum = 0.f;
+    float run = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float tv = sacc[st][r] * sc2;
-      float s = sigmoid_log2(tv);
+    for (int r = 15; r >= 0; --r) {
+      float s = sigmoid_log2(sacc[st][r] * sc2);
       if (MASKED) s = key_ok<MASKED, CAUSAL>(k0 + st * 32 + hh * 16 + r, row, Skv) ? s : 0.f;
-      sacc[st][r] = tv;
-      sg[st][r] = s;
-      sum += s;
+      run += s;
+      loc[st][r] = run;
     }
-    tot[st] = sum;
+    tot[st] = run;
   }
   // Run totals in key order (right to left): (1,1) (1,0) (0,1) (0,0), where (st, h) is
   // the 16-key run of subtile st held by wavefront half h.
@@ -95,30 +102,33 @@ __device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __re
   const float off[2] = {hh ? zst1 : zst1 + T01, hh ? zr : zr + T11};
   zr = zst0;
 
+  // Log2-domain logit relative to the current scale:
+  //   t - lam2 * (off + loc) - mb = fma(-lam2, loc, fma(s, sc2, -(mb + lam2 * off)))
+  const float mb = m2 == kNegInf ? 0.f : m2;
   float mt = kNegInf;
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
-    float run = off[st];
+    const float cst = mb + lam2 * off[st];
 #pragma unroll
-    for (int r = 15; r >= 0; --r) {
-      run += sg[st][r];
-      float av = sacc[st][r] - lam2 * run;
+    for (int r = 0; r < 16; ++r) {
+      float av = fmaf(-lam2, loc[st][r], fmaf(sacc[st][r], sc2, -cst));
       if (MASKED) av = key_ok<MASKED, CAUSAL>(k0 + st * 32 + hh * 16 + r, row, Skv) ? av : kNegInf;
       sacc[st][r] = av;
       mt = fmaxf(mt, av);
     }
   }
   mt = fmaxf(mt, other_half(mt));
-  mtrue = fmaxf(mtrue, mt);
-  const bool need = mt > m2 + kRescaleThreshold;
+  const bool need = m2 == kNegInf ? mt > kNegInf : mt > kRescaleThreshold;
   if (__any(need)) {
-    const float alpha = need ? fast_exp2(m2 - mt) : 1.f;
-    m2 = need ? mt : m2;
+    const float delta = need ? mt : 0.f;
+    const float alpha = need ? (m2 == kNegInf ? 0.f : fast_exp2(-delta)) : 1.f;
+    m2 = need ? mb + delta : m2;
     lsum *= alpha;
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) sacc[st] -= delta;
   }
-  const float mb = m2 == kNegInf ? 0.f : m2;
 
   typename M::vec8 pb[2][2];
 #pragma unroll
@@ -127,24 +137,26 @@ __device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __re
     for (int mh = 0; mh < 2; ++mh) {
       f32x8 pv;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float p = fast_exp2(sacc[st][mh * 8 + e] - mb);
-        lsum += p;
-        pv[e] = p;
-      }
+      for (int e = 0; e < 8; ++e) pv[e] = fast_exp2(sacc[st][mh * 8 + e]);
       pb[st][mh] = M::pack(pv);
+      lsum = sum8(pb[st][mh], lsum);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  // O^T[d][q] += V^T[d][key] P^T[key][q]
+  // O^T[d][q] += V^T[d][key] P^T[key][q]; A rows are keys st*32 + hh*16 + mh*8 + e.
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
 #pragma unroll
-      for (int mh = 0; mh < 2; ++mh)
-        acc[dt] = M::k16(ld_vec8(sVt + (dt * 32 + col) * C::LDV + st * 32 + hh * 16 + mh * 8),
-                         pb[st][mh], acc[dt]);
+      for (int mh = 0; mh < 2; ++mh) {
+        typename M::vec8 va;
+        if constexpr (C::kTr)
+          va = ld_kmajor<T, false>(sV, C::LDV, st * 32 + mh * 8, 16, dt * 32, lane);
+        else
+          va = ld_vec8(sV + (dt * 32 + col) * C::LDV + st * 32 + hh * 16 + mh * 8);
+        acc[dt] = M::k16(va, pb[st][mh], acc[dt]);
+      }
     }
   }
 }
@@ -154,9 +166,10 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
   using C = FwdCfg<T, D>;
   using M = Mfma<T>;
   using vec8 = typename M::vec8;
-  using Tile = TileLoader<T, D, kFwdBN>;
+  using KTile = TileLoader<T, D, kFwdBN>;
+  using VTile = TileLoader<T, D, kFwdBN, !FwdCfg<T, D>::kTr>;
   __shared__ __align__(16) T sK[kFwdBN * C::LDK];
-  __shared__ __align__(16) T sVt[D * C::LDV];
+  __shared__ __align__(16) T sV[C::V_ELEMS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, hh = lane >> 5;
@@ -187,20 +200,24 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
   const int last_key = CAUSAL ? min(q0 + kFwdBM - 1, Skv - 1) : Skv - 1;
   const int nkt = last_key / kFwdBN + 1;
 
-  Tile kt_regs, vt_regs;
+  KTile kt_regs;
+  VTile vt_regs;
   kt_regs.load(Kp, (nkt - 1) * kFwdBN, Skv, tid);
   vt_regs.load(Vp, (nkt - 1) * kFwdBN, Skv, tid);
 
   f32x16 acc[C::DT];
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
-  float m2 = kNegInf, mtrue = kNegInf, lsum = 0.f, zr = 0.f;
+  float m2 = kNegInf, lsum = 0.f, zr = 0.f;
   float* __restrict__ zb_row = args.zb + (size_t)bh * args.nZB * Sq + row;
 
   for (int kt = nkt - 1; kt >= 0; --kt) {
     __syncthreads();
     kt_regs.store_rows(sK, C::LDK, tid);
-    vt_regs.store_cols(sVt, C::LDV, tid);
+    if constexpr (C::kTr)
+      vt_regs.template store_rows<false>(sV, C::LDV, tid);
+    else
+      vt_regs.store_cols(sV, C::LDV, tid);
     __syncthreads();
     if (kt > 0) {
       kt_regs.load(Kp, (kt - 1) * kFwdBN, Skv, tid);
@@ -211,22 +228,22 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
     const bool masked = (CAUSAL && k0 + kFwdBN - 1 > wrow0) || (k0 + kFwdBN > Skv);
     float zst0, zst1;
     if (masked)
-      fwd_tile<T, D, CAUSAL, true>(sK, sVt, qf, acc, m2, mtrue, lsum, zr, zst0, zst1, k0, row, col, hh,
-                                   Skv, sc2, lam2);
+      fwd_tile<T, D, CAUSAL, true>(sK, sV, qf, acc, m2, lsum, zr, zst0, zst1, k0, row, lane, Skv, sc2,
+                                   lam2);
     else
-      fwd_tile<T, D, CAUSAL, false>(sK, sVt, qf, acc, m2, mtrue, lsum, zr, zst0, zst1, k0, row, col, hh,
-                                    Skv, sc2, lam2);
+      fwd_tile<T, D, CAUSAL, false>(sK, sV, qf, acc, m2, lsum, zr, zst0, zst1, k0, row, lane, Skv, sc2,
+                                    lam2);
     if (hh == 0 && row_ok) {
       zb_row[(size_t)(2 * kt) * Sq] = zst0;
       if (k0 + 32 < Skv) zb_row[(size_t)(2 * kt + 1) * Sq] = zst1;
     }
   }
 
-  // Renormalise to the true row max: l_true = l * 2^(m2 - mtrue).
+  // O = acc / l and LSE = m + log(l) with l = sum_j 2^(a_j - m2) >= 1 (m2 is one of
+  // the a_j and at most 8 below their max): the reference's "+1e-9" in l + 1e-9
+  // (co_alibi_fwd_kernel.py:115,120) is below fp32 resolution and is omitted.
   const float ltot = lsum + other_half(lsum);
-  const float c = m2 == kNegInf ? 0.f : fast_exp2(m2 - mtrue);
-  const float ltrue = ltot * c;
-  const float inv = c / (ltrue + 1e-9f);
+  const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
   if (row_ok) {
     T* __restrict__ Orow = static_cast<T*>(args.o) + ((size_t)bh * Sq + row) * D;
     using vec4 = typename VecOf<T, 4>::type;
@@ -239,7 +256,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
         *reinterpret_cast<vec4*>(Orow + dt * 32 + g * 8 + hh * 4) = __builtin_convertvector(v4, vec4);
       }
     }
-    if (hh == 0) args.lse[(size_t)bh * Sq + row] = (mtrue + log2f(ltrue + 1e-9f)) * kLn2;
+    if (hh == 0) args.lse[(size_t)bh * Sq + row] = ltot > 0.f ? (m2 + log2f(ltot)) * kLn2 : kNegInf;
   }
 }
 
