@@ -9,9 +9,11 @@ causal, q/k/v ~ 0.5 N(0,1), dO ~ N(0,1), seed 0), inputs resident in HBM.
 Also measured in the same run:
   * each kernel alone through the C ABI with HIP events on the launch stream
     (forward, backward pass 1, backward pass 2); the longest one is reported
-    in ``roofline`` against the dense fp16 MFMA peak;
+    in ``roofline`` against the dense fp16 MFMA peak, with the HBM traffic per
+    launch that the rocprofv3 FETCH_SIZE/WRITE_SIZE passes recorded in
+    profiles/traffic_<workload>.md (null when that file is absent);
   * the CPU baseline: the repository's CPU restatement of model.py (oracle,
-    fp32) on a bounded sample of the same workload.
+    fp32) on a time-bounded sample of the same workload.
 """
 from __future__ import annotations
 
@@ -37,8 +39,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="headline", choices=["headline", "gqa", "long", "cpu"])
-    ap.add_argument("--cpu-heads", type=int, default=16,
-                    help="query heads of batch 0 in the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="CPU work budget of the CPU-baseline sample in seconds (0 disables it)")
     ap.add_argument("--kernel-reps", type=int, default=20, help="launches per kernel in the per-kernel timing")
     return ap.parse_args()
 
@@ -54,8 +56,12 @@ def cpu_model_name() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(w, heads: int):
-    """Times the CPU oracle (fp32 restatement of model.py) on batch 0, query heads [0, heads)."""
+def cpu_baseline(w, budget_s: float):
+    """Times the CPU oracle (fp32 restatement of model.py, fwd + explicit bwd) on the same workload.
+
+    (batch, head) slices are processed in order until ``budget_s`` seconds of CPU work have been
+    spent (at least one slice); the rate is algorithmic TFLOP/s of the slices processed.
+    """
     import torch
 
     from co_alibi_attn.workloads import make_inputs
@@ -63,20 +69,26 @@ def cpu_baseline(w, heads: int):
 
     cores = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(cores)
-    q, k, v, do = (t.float() for t in make_inputs(w, seed=0, batch=1))
+    q, k, v, do = (t.float() for t in make_inputs(w, seed=0))
     lam = ref.slopes(w.heads_q, w.bias_max, dtype=w.dtype).float()
-    g = w.heads_q // w.heads_kv
-    pairs = [(0, h) for h in range(min(heads, w.heads_q))]
     scale = 1.0 / math.sqrt(w.head_dim)
-    t0 = time.perf_counter()
-    ref.forward(q, k, v, lam, causal=w.causal, scale=scale, heads=pairs)
-    ref.backward(do, q, k, v, lam, causal=w.causal, scale=scale, heads=pairs)
-    secs = time.perf_counter() - t0
-    fwd, bwd = ref.flops(1, len(pairs), w.seq, w.seq, w.head_dim, w.causal)
-    sample = (f"{w.name} workload, batch 0, query heads 0..{len(pairs) - 1} (of {w.batch}x{w.heads_q}), "
-              f"fwd+bwd fp32, {secs:.1f} s on {cores} threads of {cpu_model_name()}")
-    del g
-    return {"value": (fwd + bwd) / secs / 1e12, "unit": "TFLOPS", "cores": cores, "kind": "port",
+    done, secs = [], 0.0
+    for b in range(w.batch):
+        for h in range(w.heads_q):
+            t0 = time.perf_counter()
+            ref.forward(q, k, v, lam, causal=w.causal, scale=scale, heads=[(b, h)])
+            ref.backward(do, q, k, v, lam, causal=w.causal, scale=scale, heads=[(b, h)])
+            secs += time.perf_counter() - t0
+            done.append((b, h))
+            if secs >= budget_s:
+                break
+        if secs >= budget_s:
+            break
+    fwd, bwd = ref.flops(1, len(done), w.seq, w.seq, w.head_dim, w.causal)
+    sample = (f"{w.name} workload, {len(done)} of {w.batch * w.heads_q} (batch, head) slices "
+              f"(first: {done[0]}, last: {done[-1]}), fwd+bwd fp32, {secs:.1f} s on {cores} threads "
+              f"of {cpu_model_name()}")
+    return {"value": round((fwd + bwd) / secs / 1e12, 5), "unit": "TFLOPS", "cores": cores, "kind": "port",
             "sample": sample, "seconds": round(secs, 3)}
 
 
@@ -110,7 +122,7 @@ def main():
 
     import torch
 
-    from co_alibi_attn import _native, co_alibi_attention
+    from co_alibi_attn import co_alibi_attention
     from co_alibi_attn.workloads import WORKLOADS, make_inputs
     from oracle.co_alibi_ref import flops
 
@@ -145,64 +157,26 @@ def main():
     value = (fwd_flops + bwd_flops) / (ms_step * 1e-3) / 1e12
     print(f"[bench] {args.steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f} s)", file=sys.stderr, flush=True)
 
-    # Per-kernel timing through the C ABI on torch's current stream.
-    lib = _native.lib()
+    # Per-kernel timing through the C ABI, HIP events on the launch stream.
+    from co_alibi_attn.profiling import KERNELS, KernelSet, read_traffic
+
     B, Hq, Hkv, S, D = w.batch, w.heads_q, w.heads_kv, w.seq, w.head_dim
-    code = _native.DTYPE_CODES[w.dtype]
-    from co_alibi_attn.co_alibi_attn import _get_coalibi_slopes
-
-    lam = (2.0 * _get_coalibi_slopes(Hq, w.bias_max)).to(w.dtype).float().to(dev)
-    scale = 1.0 / math.sqrt(D)
-    qd, kd, vd = q.detach(), k.detach(), v.detach()
-    o = torch.empty_like(qd)
-    lse = torch.empty(B, Hq, S, device=dev, dtype=torch.float32)
-    zb = torch.empty(lib.co_alibi_zb_numel(B, Hq, S, S), device=dev, dtype=torch.float32)
-    ws_bytes = lib.co_alibi_bwd_workspace_bytes(B, Hq, S, S)
-    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
-    stream = torch.cuda.current_stream(dev)
-    sh = stream.cuda_stream
-    shape = (B, Hq, Hkv, S, S, D, int(w.causal), scale, sh)
-
-    def k_fwd():
-        _native.check(lib.co_alibi_fwd(code, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), lam.data_ptr(),
-                                       o.data_ptr(), lse.data_ptr(), zb.data_ptr(), *shape))
-
-    def k_dq():
-        _native.check(lib.co_alibi_bwd_dq(code, do.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
-                                          o.data_ptr(), lse.data_ptr(), zb.data_ptr(), lam.data_ptr(),
-                                          dq.data_ptr(), ws.data_ptr(), ws_bytes, *shape))
-
-    def k_dkdv():
-        _native.check(lib.co_alibi_bwd_dkdv(code, do.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
-                                            lse.data_ptr(), zb.data_ptr(), lam.data_ptr(), dk.data_ptr(),
-                                            dv.data_ptr(), ws.data_ptr(), ws_bytes, *shape))
-
-    # Issued GEMM work per launch: fwd 2 products (QK^T, PV); pass 1 three (S, dS, dQ);
-    # pass 2 four (S, dS, dV, dK), each 2*B*Hq*D per visible (query, key) pair.
-    gemm = fwd_flops / 2.0
-    kernels = {"coalibi_fwd_kernel": (k_fwd, 2 * gemm), "coalibi_bwd_dq_kernel": (k_dq, 3 * gemm),
-               "coalibi_bwd_dkdv_kernel": (k_dkdv, 4 * gemm)}
-    k_fwd()
-    k_dq()
-    k_dkdv()
+    ks = KernelSet(w, dev)
+    ks.prime()
     torch.cuda.synchronize()
     per_kernel = {}
-    for name, (fn, kflops) in kernels.items():
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(args.kernel_reps):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / args.kernel_reps
-        per_kernel[name] = {"ms": round(ms, 4), "tflops": round(kflops / (ms * 1e-3) / 1e12, 2),
-                            "issued_gflop": round(kflops / 1e9, 2)}
+    for name in KERNELS:
+        ms = ks.time(name, args.kernel_reps)
+        per_kernel[name] = {"ms": round(ms, 4),
+                            "tflops": round(ks.charged_flops(name) / (ms * 1e-3) / 1e12, 2),
+                            "charged_gflop": round(ks.charged_flops(name) / 1e9, 2),
+                            "issued_gflop": round(ks.issued_flops(name) / 1e9, 2)}
     fwd_ms = per_kernel["coalibi_fwd_kernel"]["ms"]
     bwd_ms = per_kernel["coalibi_bwd_dq_kernel"]["ms"] + per_kernel["coalibi_bwd_dkdv_kernel"]["ms"]
     dominant = max(per_kernel, key=lambda n: per_kernel[n]["ms"])
     peak = MFMA_PEAK_TFLOPS[dtype_name]
     achieved = per_kernel[dominant]["tflops"]
+    traffic = read_traffic(os.path.join(ROOT, "profiles", f"traffic_{w.name}.md")).get(dominant)
     print(f"[bench] per-kernel: {json.dumps(per_kernel)}", file=sys.stderr, flush=True)
 
     out = {
@@ -230,11 +204,12 @@ def main():
                                   "bwd": round(4 * fwd_flops / (bwd_ms * 1e-3) / 1e12, 2)},
         "kernels": per_kernel,
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(achieved / peak, 4), "traffic": None},
+                     "frac": round(achieved / peak, 4),
+                     "traffic": None if traffic is None else round(traffic)},
     }
-    if args.cpu_heads > 0:
+    if args.cpu_seconds > 0:
         print("[bench] CPU baseline ...", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(w, args.cpu_heads)
+        out["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
         out["cpu_config0_ms"] = round(cpu_config_timing(), 3)
     print(json.dumps(out), flush=True)
 

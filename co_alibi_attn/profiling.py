@@ -1,0 +1,262 @@
+"""Kernel-level measurement: C-ABI launchers over one workload's buffers, and rocprofv3 summaries.
+
+``bench.py`` times the three kernels with :class:`KernelSet`.  Run on its own,
+this file is the program that ``rocprofv3`` wraps for the counter passes, and
+it turns rocprofv3's CSV output into the short text summaries kept beside the
+benchmark:
+
+  python3 co_alibi_attn/profiling.py run --workload headline --reps 3
+      one 1 GiB device-to-device copy (the HBM-counter calibration: it reads
+      and writes exactly 1 GiB), then each kernel ``reps`` times, nothing else
+  python3 co_alibi_attn/profiling.py stats DIR --command CMD --out FILE
+      per-kernel duration table from ``rocprofv3 --kernel-trace --stats``
+  python3 co_alibi_attn/profiling.py traffic FETCH_DIR WRITE_DIR --command CMD --out FILE
+      HBM bytes per launch from a ``--pmc FETCH_SIZE`` and a ``--pmc WRITE_SIZE``
+      pass, each scaled by what the same counter reads for the calibration copy
+
+Flop accounting.  The algorithmic work is the FlashAttention convention:
+forward 2 products (QK^T, PV) and backward 5 (S, dS, dV, dQ, dK), each
+2*B*Hq*D flops per (query, key) pair, halved for causal.  The forward kernel is
+charged its 2 products.  Backward pass 2 (dK, dV) is charged S, dS, dV and dK;
+pass 1 (dQ) is charged the dQ product only, and the S and dS products it
+recomputes are counted as issued, not charged, so the charged backward work is
+exactly 2.5x the forward's.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import math
+import os
+import sys
+from collections import defaultdict
+
+if __package__ in (None, ""):
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+
+CALIBRATION_BYTES = 1 << 30
+KERNELS = ("coalibi_fwd_kernel", "coalibi_bwd_dq_kernel", "coalibi_bwd_dkdv_kernel")
+# (charged, issued) products per launch, in units of one GEMM of 2*B*Hq*D flops per visible pair.
+PRODUCTS = {"coalibi_fwd_kernel": (2, 2), "coalibi_bwd_dq_kernel": (1, 3), "coalibi_bwd_dkdv_kernel": (4, 4)}
+
+
+class KernelSet:
+    """Device buffers of one workload and a launcher per kernel, all through the C ABI on one stream."""
+
+    def __init__(self, w, device="cuda:0", seed: int = 0):
+        import torch
+
+        from co_alibi_attn import _native
+        from co_alibi_attn.co_alibi_attn import _get_coalibi_slopes
+        from co_alibi_attn.workloads import make_inputs
+
+        self.w = w
+        dev = torch.device(device)
+        lib = _native.lib()
+        B, Hq, Hkv, S, D = w.batch, w.heads_q, w.heads_kv, w.seq, w.head_dim
+        self.q, self.k, self.v, self.do = make_inputs(w, seed=seed, device=dev)
+        self.lam = (2.0 * _get_coalibi_slopes(Hq, w.bias_max)).to(w.dtype).float().to(dev)
+        self.o = torch.empty_like(self.q)
+        self.lse = torch.empty(B, Hq, S, device=dev, dtype=torch.float32)
+        self.zb = torch.empty(lib.co_alibi_zb_numel(B, Hq, S, S), device=dev, dtype=torch.float32)
+        self.ws_bytes = lib.co_alibi_bwd_workspace_bytes(B, Hq, S, S)
+        self.ws = torch.empty(self.ws_bytes, device=dev, dtype=torch.uint8)
+        self.dq, self.dk, self.dv = (torch.empty_like(t) for t in (self.q, self.k, self.v))
+        self.stream = torch.cuda.current_stream(dev)
+        code = _native.DTYPE_CODES[w.dtype]
+        shape = (B, Hq, Hkv, S, S, D, int(w.causal), 1.0 / math.sqrt(D), self.stream.cuda_stream)
+        p = lambda t: t.data_ptr()  # noqa: E731
+
+        def fwd():
+            _native.check(lib.co_alibi_fwd(code, p(self.q), p(self.k), p(self.v), p(self.lam), p(self.o),
+                                           p(self.lse), p(self.zb), *shape))
+
+        def dq():
+            _native.check(lib.co_alibi_bwd_dq(code, p(self.do), p(self.q), p(self.k), p(self.v), p(self.o),
+                                              p(self.lse), p(self.zb), p(self.lam), p(self.dq), p(self.ws),
+                                              self.ws_bytes, *shape))
+
+        def dkdv():
+            _native.check(lib.co_alibi_bwd_dkdv(code, p(self.do), p(self.q), p(self.k), p(self.v), p(self.lse),
+                                                p(self.zb), p(self.lam), p(self.dk), p(self.dv), p(self.ws),
+                                                self.ws_bytes, *shape))
+
+        self.launch = dict(zip(KERNELS, (fwd, dq, dkdv)))
+        pairs = S * S / 2.0 if w.causal else float(S * S)
+        self.gemm_flops = 2.0 * B * Hq * D * pairs
+
+    def charged_flops(self, name: str) -> float:
+        return PRODUCTS[name][0] * self.gemm_flops
+
+    def issued_flops(self, name: str) -> float:
+        return PRODUCTS[name][1] * self.gemm_flops
+
+    def prime(self) -> None:
+        """One launch of each kernel in pipeline order, so every input of every kernel is defined."""
+        for name in KERNELS:
+            self.launch[name]()
+
+    def time(self, name: str, reps: int) -> float:
+        """Average launch duration in ms over ``reps`` back-to-back launches, HIP events on the launch stream."""
+        import torch
+
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        for _ in range(reps):
+            self.launch[name]()
+        e1.record(self.stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+
+def calibration_copy(device="cuda:0", nbytes: int = CALIBRATION_BYTES) -> None:
+    """A device-to-device copy of ``nbytes``: it reads and writes exactly ``nbytes`` of HBM."""
+    import torch
+
+    a = torch.ones(nbytes // 2, dtype=torch.float16, device=device)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def cmd_run(args) -> None:
+    import torch
+
+    from co_alibi_attn.workloads import WORKLOADS
+
+    calibration_copy()
+    ks = KernelSet(WORKLOADS[args.workload])
+    for _ in range(args.reps):
+        ks.prime()
+    torch.cuda.synchronize()
+    print(f"profiling run: {args.workload}, {args.reps} launches of each of {', '.join(KERNELS)}", flush=True)
+
+
+def _csv_rows(directory: str, suffix: str):
+    files = sorted(glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {directory}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def _short(name: str) -> str:
+    for k in KERNELS:
+        if k in name:
+            return k
+    return name if len(name) <= 60 else name[:57] + "..."
+
+
+def cmd_stats(args) -> None:
+    rows = _csv_rows(args.dir, "kernel_stats.csv")
+    lines = [f"# rocprofv3 kernel statistics: {args.title}", "", "Command (R is the repository root on the GPU box):", "",
+             "```", args.command, "```", "",
+             "The summary is written by `python3 co_alibi_attn/profiling.py stats <rocprofv3 output dir>`.", "",
+             "| kernel | calls | average (us) | min (us) | max (us) | share of GPU time |",
+             "|---|---:|---:|---:|---:|---:|"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        lines.append(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                     f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} % |")
+    _write(args.out, lines)
+
+
+def _per_dispatch(directory: str, counter: str):
+    """{kernel name: [counter value per dispatch]} (values of one dispatch summed over their instances)."""
+    acc = defaultdict(float)
+    names = {}
+    for r in _csv_rows(directory, "counter_collection.csv"):
+        if r["Counter_Name"] != counter:
+            continue
+        key = (r["Process_Id"], r["Dispatch_Id"])
+        acc[key] += float(r["Counter_Value"])
+        names[key] = r["Kernel_Name"]
+    out = defaultdict(list)
+    for key, val in acc.items():
+        out[names[key]].append(val)
+    return out
+
+
+def cmd_traffic(args) -> None:
+    lines = [f"# HBM traffic per launch: {args.title}", "", "Commands (R is the repository root on the GPU box):", "",
+             "```", args.command, "```", "",
+             f"Each counter is read in KiB per dispatch and scaled by the factor that makes the calibration copy "
+             f"(a {CALIBRATION_BYTES >> 20} MiB device-to-device copy, `__amd_rocclr_copyBuffer`, the copy "
+             f"dispatch with the largest reading) read exactly {CALIBRATION_BYTES >> 20} MiB. The summary is written "
+             f"by `python3 co_alibi_attn/profiling.py traffic <fetch dir> <write dir>`.", ""]
+    result = {}
+    for counter, directory in (("FETCH_SIZE", args.fetch_dir), ("WRITE_SIZE", args.write_dir)):
+        per = _per_dispatch(directory, counter)
+        copies = [v for n, vals in per.items() if "copyBuffer" in n for v in vals]
+        if not copies:
+            raise SystemExit(f"no calibration copy dispatch in {directory}")
+        cal_kib = max(copies)
+        factor = CALIBRATION_BYTES / (cal_kib * 1024.0)
+        lines.append(f"- `{counter}`: calibration copy read {cal_kib:.0f} KiB, factor {factor:.4f}")
+        for name, vals in per.items():
+            k = _short(name)
+            if k in KERNELS:
+                result.setdefault(k, {})[counter] = sum(vals) / len(vals) * 1024.0 * factor
+    lines += ["", "| kernel | fetched (MB) | written (MB) | HBM traffic (MB) |", "|---|---:|---:|---:|"]
+    for k in KERNELS:
+        if k in result:
+            f, wr = result[k].get("FETCH_SIZE", 0.0), result[k].get("WRITE_SIZE", 0.0)
+            lines.append(f"| `{k}` | {f / 1e6:.1f} | {wr / 1e6:.1f} | {(f + wr) / 1e6:.1f} |")
+    lines += ["", "Machine-readable (bytes per launch, read by bench.py):", ""]
+    for k in KERNELS:
+        if k in result:
+            total = result[k].get("FETCH_SIZE", 0.0) + result[k].get("WRITE_SIZE", 0.0)
+            lines.append(f"    traffic_bytes_per_launch {k} {total:.0f}")
+    _write(args.out, lines)
+
+
+def read_traffic(path: str):
+    """{kernel: HBM bytes per launch} from a summary written by ``traffic`` (empty if the file is absent)."""
+    out = {}
+    if not os.path.exists(path):
+        return out
+    with open(path) as fh:
+        for line in fh:
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch":
+                out[parts[1]] = float(parts[2])
+    return out
+
+
+def _write(path: str, lines) -> None:
+    text = "\n".join(lines) + "\n"
+    if path == "-":
+        sys.stdout.write(text)
+        return
+    with open(path, "w") as fh:
+        fh.write(text)
+    print(f"wrote {path}")
+
+
+def main(argv=None) -> None:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    r = sub.add_parser("run")
+    r.add_argument("--workload", default="headline")
+    r.add_argument("--reps", type=int, default=3)
+    s = sub.add_parser("stats")
+    s.add_argument("dir")
+    s.add_argument("--command", required=True)
+    s.add_argument("--title", default="headline benchmark")
+    s.add_argument("--out", default="-")
+    t = sub.add_parser("traffic")
+    t.add_argument("fetch_dir")
+    t.add_argument("write_dir")
+    t.add_argument("--command", required=True)
+    t.add_argument("--title", default="headline workload")
+    t.add_argument("--out", default="-")
+    args = ap.parse_args(argv)
+    {"run": cmd_run, "stats": cmd_stats, "traffic": cmd_traffic}[args.cmd](args)
+
+
+if __name__ == "__main__":
+    main()
