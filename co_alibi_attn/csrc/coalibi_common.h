@@ -90,6 +90,23 @@ __device__ __forceinline__ float half_wave_prefix(float x) {
   return x;
 }
 
+// Word 3 of a gfx9-family buffer resource for raw (stride 0) dword access: 32-bit data
+// format, no swizzle.  Loads at offsets >= num_records return zero.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+// Buffer resource over `elems` elements at `p`.  Both are wave-uniform at every call site;
+// readfirstlane states that to the compiler, which otherwise wraps each load in a loop over
+// the distinct resource values of the wave.
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const T* p, int elems) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(p);
+  const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a));
+  const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a >> 32));
+  const int bytes = __builtin_amdgcn_readfirstlane(elems * (int)sizeof(T));
+  void* base = reinterpret_cast<void*>((static_cast<unsigned long long>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, bytes, kBufferRsrcWord3);
+}
+
 // 16-byte global / LDS accessors.
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
@@ -150,16 +167,18 @@ struct TileLoader {
   __device__ __forceinline__ static int grp_row(int g) { return GROUPED ? (g % (ROWS / KG)) * KG : g / CPR; }
   __device__ __forceinline__ static int grp_col(int g) { return GROUPED ? (g / (ROWS / KG)) * CH : (g % CPR) * CH; }
 
+  // Rows row0 .. row0+ROWS-1 of a row-major [nrows][D] array; rows >= nrows read as zero.
+  // Buffer loads: the resource covers exactly the tile's valid rows, so the hardware range
+  // check zero-fills the rest; per-lane offsets are tile-invariant and the base is uniform.
   __device__ __forceinline__ void load(const T* __restrict__ base, int row0, int nrows, int tid) {
+    const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(base + (size_t)row0 * D, min(max(nrows - row0, 0), ROWS) * D);
 #pragma unroll
     for (int i = 0; i < GPT; ++i) {
       const int g = tid + 256 * i;
       const int rr = grp_row(g), cc = grp_col(g);
 #pragma unroll
-      for (int k = 0; k < KG; ++k) {
-        const int row = row0 + rr + k;
-        r[i][k] = row < nrows ? ld16(base + (size_t)row * D + cc) : u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int k = 0; k < KG; ++k)
+        r[i][k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, ((rr + k) * D + cc) * (int)sizeof(T), 0, 0);
     }
   }
 
