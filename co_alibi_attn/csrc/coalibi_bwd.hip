@@ -137,9 +137,9 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_bwd_dq_ke
   const int col = lane & 31, hh = lane >> 5;
   const int Sq = args.Sq, Skv = args.Skv;
   const int nQB = (Sq + kBM - 1) / kBM;
-  const int wid = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = wid / nQB;
-  const int qb = nQB - 1 - (wid - bh * nQB);
+  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hq);
+  const int bh = item.head;
+  const int qb = nQB - 1 - item.rank;  // rank 0: the longest causal rows
   const int b = bh / args.Hq, hq = bh - b * args.Hq;
   const int hkv = hq / (args.Hq / args.Hkv);
   const size_t qoff = (size_t)bh * Sq * D;
@@ -277,9 +277,9 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_kernel(BwdArgs args) 
   const int col = lane & 31, hh = lane >> 5;
   const int Sq = args.Sq, Skv = args.Skv;
   const int nKB = (Skv + kBK - 1) / kBK;
-  const int wid = xcd_remap(blockIdx.x, gridDim.x);
-  const int bhk = wid / nKB;               // b * Hkv + hkv
-  const int kb = wid - bhk * nKB;          // small kb = most query rows first
+  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hkv);
+  const int bhk = item.head;               // b * Hkv + hkv
+  const int kb = item.rank;                // rank 0: key block 0, seen by the most query rows
   const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;
   const int group = args.Hq / args.Hkv;
   const size_t kvoff = (size_t)bhk * Skv * D;

@@ -78,18 +78,6 @@ __device__ __forceinline__ float sigmoid_log2(float t) { return fast_rcp(1.0f + 
 // Value held by the lane in the other half of the wavefront (l ^ 32).
 __device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32); }
 
-// Inclusive prefix sum across the 32 lanes of each wavefront half
-// (lanes 0..31 and 32..63 are independent segments).
-__device__ __forceinline__ float half_wave_prefix(float x) {
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));  // row_shr:1
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, true));  // row_shr:2
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, true));  // row_shr:4
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, true));  // row_shr:8
-  // row_bcast:15 into rows 1 and 3: lanes 16..31 (48..63) add lane 15 (47).
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));
-  return x;
-}
-
 // Word 3 of a gfx9-family buffer resource for raw (stride 0) dword access: 32-bit data
 // format, no swizzle.  Loads at offsets >= num_records return zero.
 constexpr int kBufferRsrcWord3 = 0x00020000;
@@ -124,15 +112,18 @@ __device__ __forceinline__ typename Mfma<T>::vec8 zero_vec8() {
   return z;
 }
 
-// Work-group id -> logical work item.  Consecutive work-group ids are
-// dispatched round-robin over the 8 XCDs; this remap makes consecutive logical
-// items run on the same XCD so that the tiles sharing one head's K/V (or Q/dO)
-// are served from one L2.
-__device__ __forceinline__ int xcd_remap(int id, int n) {
-  constexpr int kXcd = 8;
-  if (n % kXcd != 0) return id;
-  return (id % kXcd) * (n / kXcd) + id / kXcd;
-}
+// Work order of a grid of row or key blocks over `heads` (batch, head) pairs.  Ids are
+// taken rank-major, head-minor, where rank 0 is the block with
+// the most work (the longest causal rows, or the key block seen by the most query rows).
+// The dispatcher hands consecutive work-group ids to the 8 XCDs in turn, so every XCD sees
+// its blocks in decreasing cost (longest-processing-time-first list scheduling keeps the
+// tail short) and, when `heads` is a multiple of 8, all blocks of a head run on one XCD and
+// share its L2.
+struct WorkItem {
+  int head;  // b * heads_per_batch + h
+  int rank;  // 0 = most work
+};
+__device__ __forceinline__ WorkItem lpt_item(int id, int heads) { return {id % heads, id / heads}; }
 
 }  // namespace coalibi
 

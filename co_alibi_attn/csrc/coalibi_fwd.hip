@@ -175,9 +175,9 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
   const int col = lane & 31, hh = lane >> 5;
   const int Sq = args.Sq, Skv = args.Skv;
   const int nQB = (Sq + kFwdBM - 1) / kFwdBM;
-  const int wid = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = wid / nQB;
-  const int qb = nQB - 1 - (wid - bh * nQB);  // longest causal rows first
+  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hq);
+  const int bh = item.head;
+  const int qb = nQB - 1 - item.rank;  // rank 0: the longest causal rows
   const int b = bh / args.Hq, hq = bh - b * args.Hq;
   const int hkv = hq / (args.Hq / args.Hkv);
   const T* __restrict__ Qp = static_cast<const T*>(args.q) + (size_t)bh * Sq * D;
