@@ -253,11 +253,13 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_bwd_dq_ke
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2: dK, dV.  Per wavefront the 32 keys kw0.. of one 32-key block, held as
-// MFMA A operands (row R <-> key kw0 + kRowOfReg(R)) so that register r of lane
-// (col, hh) of S^T <-> key kw0 + hh*16 + r, query q0 + sq*32 + col.
+// Pass 2, fp32 validation mode: dK, dV.  Per wavefront the 32 keys kw0.. of one
+// 32-key block, held as MFMA A operands (row R <-> key kw0 + kRowOfReg(R)) so that
+// register r of lane (col, hh) of S^T <-> key kw0 + hh*16 + r, query q0 + sq*32 + col.
+// The 16-bit kernel below splits this work over wavefront pairs; fp32 tiles with
+// their transposed copies do not fit the LDS that split needs.
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_kernel(BwdArgs args) {
+__global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs args) {
   using C = BwdCfg<T, D>;
   using M = Mfma<T>;
   using vec8 = typename M::vec8;
@@ -446,6 +448,259 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_kernel(BwdArgs args) 
   }
 }
 
+
+// Pass 2 for fp16/bf16: dK, dV with wavefront pairs.  A work-group of 8
+// wavefronts owns 128 keys in four key groups kg of 32 and walks query tiles of 64
+// rows.  Wavefront (kg, qh) holds K and V of its key group as MFMA A operands (as
+// above) and computes S^T, dS^T and then s, dP for query half qh of the tile into
+// its key group's LDS buffer.  After a barrier each wavefront of the pair reduces
+// over all 64 queries of the tile, but only for its half of the head dim:
+//   dV^T[d][key] += dO^T[d][q] s[q][key],  dK^T[d][key] += Q^T[d][q] dP[q][key],
+// for d in [qh*D/2, qh*D/2 + D/2).  Splitting the accumulators and the score tile
+// this way halves the registers of the one-wavefront-per-key-group form, which
+// gives two wavefronts per SIMD at no extra elementwise work.  Q and dO tiles
+// arrive by buffer-to-LDS DMA into a second buffer while the current tile is in
+// use, so no registers hold the next tile; K stays in registers and V is read from
+// LDS (both in full would not fit the register budget at D = 128).
+constexpr int kPairBK = 128;    // keys per work-group
+constexpr int kPairBQ = 64;     // query rows per tile
+constexpr int kPairWaves = 8;   // wavefronts per work-group: 4 key groups x 2 query halves
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(BwdArgs args) {
+  static_assert(sizeof(T) == 2, "the wavefront-pair pass 2 is the 16-bit path");
+  using C = BwdCfg<T, D>;
+  using M = Mfma<T>;
+  using vec8 = typename M::vec8;
+  constexpr int BQ = kPairBQ;
+  constexpr int NKG = kPairBK / 32;
+  constexpr int DH = C::DT / 2;                   // 32-row tiles of d per wavefront
+  constexpr int TILE = BQ * C::LDR;               // elements of one padded Q or dO tile
+  constexpr int CPR = C::LDR * (int)sizeof(T) / 16;  // 16-byte chunks per padded LDS row
+  constexpr int NDMA = BQ * CPR / 64;             // wavefront DMA instructions per tile
+  constexpr int DMA_SLOTS = (NDMA + kPairWaves - 1) / kPairWaves;
+  static_assert(BQ * CPR % 64 == 0, "tile must split into whole DMA instructions");
+  constexpr int LDSP = 32 + C::CH;  // s / dP rows: 32 keys + one 16-byte pad
+  __shared__ __align__(16) T sQ[2][TILE];
+  __shared__ __align__(16) T sdO[2][TILE];
+  __shared__ __align__(16) T sV[kPairBK * C::LDR];       // V rows, permuted per 32-key group
+  __shared__ __align__(16) T sSP[NKG][2][BQ * LDSP];     // per key group: s and dP, [q][key]
+  __shared__ __align__(16) float sLse2[2][BQ];
+  __shared__ __align__(16) float sDsum[2][BQ];
+  __shared__ __align__(16) float sZb[2][NKG][BQ];
+  __shared__ __align__(16) float sCb[2][NKG][BQ];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 31, hh = lane >> 5;
+  const int kg = wave >> 1, qh = wave & 1;
+  const int Sq = args.Sq, Skv = args.Skv;
+  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hkv);
+  const int bhk = item.head;               // b * Hkv + hkv
+  const int kb = item.rank;                // rank 0: key block 0, seen by the most query rows
+  const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;
+  const int group = args.Hq / args.Hkv;
+  const size_t kvoff = (size_t)bhk * Skv * D;
+  const int kw0 = kb * kPairBK + kg * 32;  // first key of this wavefront's key group
+  const int key0 = kw0 + hh * 16;          // key of register 0 of this lane
+  const bool keys_ok = kw0 < Skv;
+  T* __restrict__ sS = sSP[kg][0];
+  T* __restrict__ sP = sSP[kg][1];
+
+  // Zero both tile buffers once: DMA slots past the last query row then hold zeros.
+  {
+    u32x4* z = reinterpret_cast<u32x4*>(&sQ[0][0]);
+    for (int i = tid; i < 2 * TILE * (int)sizeof(T) / 16; i += 64 * kPairWaves) z[i] = u32x4{0u, 0u, 0u, 0u};
+    z = reinterpret_cast<u32x4*>(&sdO[0][0]);
+    for (int i = tid; i < 2 * TILE * (int)sizeof(T) / 16; i += 64 * kPairWaves) z[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+
+  vec8 ka[C::KS];
+  {
+    const int key = kw0 + kRowOfReg(col);
+    const bool key_ok = key < Skv;
+    const T* __restrict__ Kr = static_cast<const T*>(args.k) + kvoff + (size_t)key * D;
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) ka[ks] = key_ok ? ld_vec8(Kr + ks * 16 + hh * 8) : zero_vec8<T>();
+  }
+  // V rows of the work-group's keys; LDS row R of each 32-row group holds key
+  // kRowOfReg(R) of the group, the A-operand order.
+  {
+    const int kbase = kb * kPairBK;
+    const T* __restrict__ Vp = static_cast<const T*>(args.v) + kvoff;
+    for (int g = tid; g < kPairBK * (D / 8); g += 64 * kPairWaves) {
+      const int r = g / (D / 8), c = (g - r * (D / 8)) * 8;
+      const int key = kbase + (r & ~31) + kRowOfReg(r & 31);
+      st16(sV + r * C::LDR + c, key < Skv ? ld16(Vp + (size_t)key * D + c) : u32x4{0u, 0u, 0u, 0u});
+    }
+  }
+  const T* __restrict__ sVg = sV + kg * 32 * C::LDR;
+
+  f32x16 dk[DH], dv[DH];
+#pragma unroll
+  for (int i = 0; i < DH; ++i) {
+    dk[i] = f32x16{};
+    dv[i] = f32x16{};
+  }
+
+  // DMA source offsets of this lane for its instruction slots: slot m is tile chunk
+  // c = (wave + 8m)*64 + lane, i.e. padded row c / CPR, chunk c % CPR; pad chunks
+  // point past the resource and read as zero.
+  int dma_off[DMA_SLOTS];
+#pragma unroll
+  for (int m = 0; m < DMA_SLOTS; ++m) {
+    const int c = (wave + kPairWaves * m) * 64 + lane;
+    const int row = c / CPR, j = c - row * CPR;
+    dma_off[m] = j < D / 8 ? (row * D + j * 8) * (int)sizeof(T) : 0x40000000;
+  }
+
+  // Work list: (query head gi, query tile qt) pairs.
+  const int nQT = (Sq + BQ - 1) / BQ;
+  const int qt0 = CAUSAL ? min((kb * kPairBK) / BQ, nQT) : 0;
+  const int per_head = nQT - qt0;
+  const int nwork = per_head * group;
+  const int jb = kw0 / 32;  // this key group's 32-key block
+  auto issue_tile = [&](int w, int buf) {
+    const int gi = w / per_head, qt = qt0 + (w - gi * per_head);
+    const size_t qoff = ((size_t)(b * args.Hq + hkv * group + gi) * Sq + (size_t)qt * BQ) * D;
+    const int elems = min(max(Sq - qt * BQ, 0), BQ) * D;
+    const __amdgpu_buffer_rsrc_t rq = tile_rsrc(static_cast<const T*>(args.q) + qoff, elems);
+    const __amdgpu_buffer_rsrc_t rd = tile_rsrc(static_cast<const T*>(args.dout) + qoff, elems);
+#pragma unroll
+    for (int m = 0; m < DMA_SLOTS; ++m) {
+      const int i = wave + kPairWaves * m;
+      if (i < NDMA) {
+        dma16_to_lds(rq, &sQ[buf][i * 64 * 16 / (int)sizeof(T)], dma_off[m]);
+        dma16_to_lds(rd, &sdO[buf][i * 64 * 16 / (int)sizeof(T)], dma_off[m]);
+      }
+    }
+  };
+  // Per-row statistics of a tile, one value per lane (= tile row) through buffer
+  // loads (rows past Sq and blocks past the last read as zero): wavefront 0 loads
+  // LSE, wavefront 1 loads D, and the two wavefronts of a key group load its zb and cb.
+  float st_a = 0.f, st_b = 0.f;
+  auto load_stats = [&](int w) {
+    const int gi = w / per_head, qt = qt0 + (w - gi * per_head);
+    const size_t bh = (size_t)b * args.Hq + hkv * group + gi;
+    const int q0 = qt * BQ;
+    const int rows = min(max(Sq - q0, 0), BQ);
+    if (wave < 2) {
+      const float* src = (wave == 0 ? args.lse : args.dsum) + bh * Sq + q0;
+      st_a = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(src, rows), lane * 4, 0, 0));
+    }
+    const float* blk = (qh == 0 ? args.zb : args.cb) + (bh * args.nZB + jb) * Sq + q0;
+    st_b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(blk, jb < args.nZB ? rows : 0),
+                                                                          lane * 4, 0, 0));
+  };
+  auto store_stats = [&](int buf) {
+    if (wave == 0) sLse2[buf][lane] = st_a * kLog2e;
+    if (wave == 1) sDsum[buf][lane] = st_a;
+    if (qh == 0) sZb[buf][kg][lane] = st_b;
+    else sCb[buf][kg][lane] = st_b;
+  };
+
+  __syncthreads();  // zeroed tiles before the first DMA lands
+  if (nwork > 0) {
+    issue_tile(0, 0);
+    load_stats(0);
+    __builtin_amdgcn_s_waitcnt(0);  // the stats loads have to land before they are stored
+    store_stats(0);
+  }
+
+  for (int w = 0; w < nwork; ++w) {
+    const int buf = w & 1;
+    const int gi = w / per_head, qt = qt0 + (w - gi * per_head);
+    const int hq = hkv * group + gi;
+    const float lam = args.slopes[hq];
+    const float lam2 = lam * kLog2e;
+    const int q0 = qt * BQ;
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's DMA of tile w (and stats of tile w+1 issued last round)
+    __syncthreads();                // every wavefront's DMA landed; tile w-1 is no longer read
+    if (w + 1 < nwork) {
+      issue_tile(w + 1, buf ^ 1);
+      load_stats(w + 1);
+    }
+    const T* __restrict__ tQ = sQ[buf];
+    const T* __restrict__ tdO = sdO[buf];
+
+    // Query half h of the tile meets this key group (some pair is visible).
+    auto half_live = [&](int h) {
+      const int qs0 = q0 + h * 32;
+      return keys_ok && qs0 < Sq && (!CAUSAL || qs0 + 31 >= kw0);
+    };
+    if (half_live(qh)) {
+      const int qs0 = q0 + qh * 32;
+      const bool masked = (CAUSAL && qs0 < kw0 + 31) || (qs0 + 32 > Sq) || (kw0 + 32 > Skv);
+      const int ql = qh * 32 + col;  // tile-local query row of this lane
+      const int row = qs0 + col;
+      f32x16 sacc = f32x16{}, dacc = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks) {
+        sacc = M::k16(ka[ks], ld_vec8(tQ + ql * C::LDR + ks * 16 + hh * 8), sacc);
+        dacc = M::k16(ld_vec8(sVg + col * C::LDR + ks * 16 + hh * 8), ld_vec8(tdO + ql * C::LDR + ks * 16 + hh * 8),
+                      dacc);
+        // Bound the operand reads in flight: hoisting all of them costs more
+        // registers than two wavefronts per SIMD leave.
+        if (ks % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+      }
+      vec8 sb[2], pb[2];
+      float atot;
+      if (masked)
+        dp_tile<T, true, CAUSAL>(sacc, dacc, sZb[buf][kg][ql], sCb[buf][kg][ql], sLse2[buf][ql], sDsum[buf][ql],
+                                 key0, row, hh, Skv, Sq, args.sc2, lam, lam2, sb, pb, atot);
+      else
+        dp_tile<T, false, CAUSAL>(sacc, dacc, sZb[buf][kg][ql], sCb[buf][kg][ql], sLse2[buf][ql], sDsum[buf][ql],
+                                  key0, row, hh, Skv, Sq, args.sc2, lam, lam2, sb, pb, atot);
+      *reinterpret_cast<vec8*>(sS + ql * LDSP + hh * 16) = sb[0];
+      *reinterpret_cast<vec8*>(sS + ql * LDSP + hh * 16 + 8) = sb[1];
+      *reinterpret_cast<vec8*>(sP + ql * LDSP + hh * 16) = pb[0];
+      *reinterpret_cast<vec8*>(sP + ql * LDSP + hh * 16 + 8) = pb[1];
+    }
+    __syncthreads();
+    // Reduce over the live query halves: reduction rows h*32 + mh*16 + kh*8 + e.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (!half_live(h)) continue;
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh) {
+        const vec8 sop = ld_kmajor<T, false>(sS, LDSP, h * 32 + mh * 16, 8, 0, lane);
+        const vec8 pop = ld_kmajor<T, false>(sP, LDSP, h * 32 + mh * 16, 8, 0, lane);
+#pragma unroll
+        for (int i = 0; i < DH; ++i) {
+          const int dt = qh * DH + i;
+          const vec8 doa = ld_kmajor<T, false>(tdO, C::LDR, h * 32 + mh * 16, 8, dt * 32, lane);
+          const vec8 qa = ld_kmajor<T, false>(tQ, C::LDR, h * 32 + mh * 16, 8, dt * 32, lane);
+          dv[i] = M::k16(doa, sop, dv[i]);
+          dk[i] = M::k16(qa, pop, dk[i]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // Statistics of tile w+1 (loaded during this tile) into the other buffer; that
+    // buffer was last read in tile w-1.
+    if (w + 1 < nwork) store_stats(buf ^ 1);
+  }
+
+  const int key = kw0 + col;
+  if (key < Skv) {
+    using vec4 = typename VecOf<T, 4>::type;
+    T* __restrict__ dKr = static_cast<T*>(args.dk) + kvoff + (size_t)key * D;
+    T* __restrict__ dVr = static_cast<T*>(args.dv) + kvoff + (size_t)key * D;
+    const float sc = args.sm_scale;
+#pragma unroll
+    for (int i = 0; i < DH; ++i) {
+      const int dt = qh * DH + i;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = dt * 32 + g * 8 + hh * 4;
+        f32x4 k4 = {dk[i][g * 4 + 0] * sc, dk[i][g * 4 + 1] * sc, dk[i][g * 4 + 2] * sc, dk[i][g * 4 + 3] * sc};
+        f32x4 v4 = {dv[i][g * 4 + 0], dv[i][g * 4 + 1], dv[i][g * 4 + 2], dv[i][g * 4 + 3]};
+        *reinterpret_cast<vec4*>(dKr + c0) = __builtin_convertvector(k4, vec4);
+        *reinterpret_cast<vec4*>(dVr + c0) = __builtin_convertvector(v4, vec4);
+      }
+    }
+  }
+}
+
 }  // namespace
 
 template <typename T, int D, bool CAUSAL>
@@ -457,9 +712,15 @@ hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream) {
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
-    const int nKB = (a.Skv + kBK - 1) / kBK;
-    hipLaunchKernelGGL((coalibi_bwd_dkdv_kernel<T, D, CAUSAL>), dim3(nKB * a.B * a.Hkv), dim3(256), 0, stream,
-                       a);
+    if constexpr (sizeof(T) == 2) {
+      const int nKB = (a.Skv + kPairBK - 1) / kPairBK;
+      hipLaunchKernelGGL((coalibi_bwd_dkdv_kernel<T, D, CAUSAL>), dim3(nKB * a.B * a.Hkv), dim3(64 * kPairWaves),
+                         0, stream, a);
+    } else {
+      const int nKB = (a.Skv + kBK - 1) / kBK;
+      hipLaunchKernelGGL((coalibi_bwd_dkdv_f32_kernel<T, D, CAUSAL>), dim3(nKB * a.B * a.Hkv), dim3(256), 0,
+                         stream, a);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

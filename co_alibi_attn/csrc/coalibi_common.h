@@ -95,6 +95,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const T* p, int elem
   return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, bytes, kBufferRsrcWord3);
 }
 
+// 16-byte buffer-to-LDS DMA: lane i of the wavefront writes the 16 bytes at byte offset
+// `voffset` of the resource to LDS address lds + 16*i (offsets past the resource read as
+// zero).  `lds` must be wave-uniform.  A plain function: inside kernel templates the
+// builtin does not survive the host compilation pass.
+__device__ __forceinline__ void dma16_to_lds(__amdgpu_buffer_rsrc_t rsrc, void* lds, int voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+}
+
 // 16-byte global / LDS accessors.
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
