@@ -559,8 +559,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(Bw
   const int per_head = nQT - qt0;
   const int nwork = per_head * group;
   const int jb = kw0 / 32;  // this key group's 32-key block
-  auto issue_tile = [&](int w, int buf) {
-    const int gi = w / per_head, qt = qt0 + (w - gi * per_head);
+  auto issue_tile = [&](int gi, int qt, int buf) {
     const size_t qoff = ((size_t)(b * args.Hq + hkv * group + gi) * Sq + (size_t)qt * BQ) * D;
     const int elems = min(max(Sq - qt * BQ, 0), BQ) * D;
     const __amdgpu_buffer_rsrc_t rq = tile_rsrc(static_cast<const T*>(args.q) + qoff, elems);
@@ -578,8 +577,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(Bw
   // loads (rows past Sq and blocks past the last read as zero): wavefront 0 loads
   // LSE, wavefront 1 loads D, and the two wavefronts of a key group load its zb and cb.
   float st_a = 0.f, st_b = 0.f;
-  auto load_stats = [&](int w) {
-    const int gi = w / per_head, qt = qt0 + (w - gi * per_head);
+  auto load_stats = [&](int gi, int qt) {
     const size_t bh = (size_t)b * args.Hq + hkv * group + gi;
     const int q0 = qt * BQ;
     const int rows = min(max(Sq - q0, 0), BQ);
@@ -600,15 +598,17 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(Bw
 
   __syncthreads();  // zeroed tiles before the first DMA lands
   if (nwork > 0) {
-    issue_tile(0, 0);
-    load_stats(0);
+    issue_tile(0, qt0, 0);
+    load_stats(0, qt0);
     __builtin_amdgcn_s_waitcnt(0);  // the stats loads have to land before they are stored
     store_stats(0);
   }
 
+  int gi = 0, qt = qt0;  // current work item; the next one is (gn, qn)
   for (int w = 0; w < nwork; ++w) {
     const int buf = w & 1;
-    const int gi = w / per_head, qt = qt0 + (w - gi * per_head);
+    const bool wrap = qt + 1 == nQT;
+    const int gn = wrap ? gi + 1 : gi, qn = wrap ? qt0 : qt + 1;
     const int hq = hkv * group + gi;
     const float lam = args.slopes[hq];
     const float lam2 = lam * kLog2e;
@@ -616,8 +616,8 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(Bw
     __builtin_amdgcn_s_waitcnt(0);  // this wavefront's DMA of tile w (and stats of tile w+1 issued last round)
     __syncthreads();                // every wavefront's DMA landed; tile w-1 is no longer read
     if (w + 1 < nwork) {
-      issue_tile(w + 1, buf ^ 1);
-      load_stats(w + 1);
+      issue_tile(gn, qn, buf ^ 1);
+      load_stats(gn, qn);
     }
     const T* __restrict__ tQ = sQ[buf];
     const T* __restrict__ tdO = sdO[buf];
@@ -638,9 +638,6 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(Bw
         sacc = M::k16(ka[ks], ld_vec8(tQ + ql * C::LDR + ks * 16 + hh * 8), sacc);
         dacc = M::k16(ld_vec8(sVg + col * C::LDR + ks * 16 + hh * 8), ld_vec8(tdO + ql * C::LDR + ks * 16 + hh * 8),
                       dacc);
-        // Bound the operand reads in flight: hoisting all of them costs more
-        // registers than two wavefronts per SIMD leave.
-        if (ks % 2 == 1) __builtin_amdgcn_sched_barrier(0);
       }
       vec8 sb[2], pb[2];
       float atot;
@@ -672,12 +669,13 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(Bw
           dv[i] = M::k16(doa, sop, dv[i]);
           dk[i] = M::k16(qa, pop, dk[i]);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
     // Statistics of tile w+1 (loaded during this tile) into the other buffer; that
     // buffer was last read in tile w-1.
     if (w + 1 < nwork) store_stats(buf ^ 1);
+    gi = gn;
+    qt = qn;
   }
 
   const int key = kw0 + col;
