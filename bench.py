@@ -38,10 +38,13 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="headline", choices=["headline", "gqa", "long", "cpu"])
+    ap.add_argument("--workload", default="headline", choices=["headline", "gqa", "long", "cpu", "gpt"],
+                    help="attention workload (BASELINE configs[0..3]) or the GPT training step (configs[4])")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="CPU work budget of the CPU-baseline sample in seconds (0 disables it)")
     ap.add_argument("--kernel-reps", type=int, default=20, help="launches per kernel in the per-kernel timing")
+    ap.add_argument("--no-sdpa", dest="sdpa", action="store_false",
+                    help="skip the torch SDPA (plain causal attention) comparison")
     return ap.parse_args()
 
 
@@ -113,12 +116,73 @@ def cpu_config_timing():
     return times[len(times) // 2] * 1e3
 
 
+def gpt_bench(args) -> None:
+    """one GPT training step (fwd + bwd + AdamW) per step, bf16 autocast."""
+    import torch
+
+    from co_alibi_attn.gpt import GPT, GPTConfig, make_optimizer, synthetic_batch, train_step
+
+    cfg, batch, seq = GPTConfig(), 8, 1024
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    model = GPT(cfg).to(dev)
+    opt = make_optimizer(model)
+    idx, tgt = synthetic_batch(cfg, batch, seq, seed=0, device=dev)
+    print(f"[bench] GPT {cfg.n_layer}L d{cfg.d_model} H{cfg.n_head} vocab {cfg.vocab}: "
+          f"{model.n_params() / 1e6:.1f}M params, B{batch} S{seq}", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        train_step(model, opt, idx, tgt)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        loss = train_step(model, opt, idx, tgt)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    # Attention alone at the same shape (fwd + bwd), to state its share of the step.
+    from co_alibi_attn import co_alibi_attention
+
+    hd = cfg.d_model // cfg.n_head
+    gen = torch.Generator().manual_seed(1)
+    q, k, v, do = (torch.randn(batch, cfg.n_head, seq, hd, generator=gen).to(torch.bfloat16).to(dev)
+                   for _ in range(4))
+    q.requires_grad_(True), k.requires_grad_(True), v.requires_grad_(True)
+    for _ in range(3):
+        co_alibi_attention(q, k, v).backward(do)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(10):
+        co_alibi_attention(q, k, v).backward(do)
+    end.record()
+    torch.cuda.synchronize()
+    attn_ms = start.elapsed_time(end) / 10 * cfg.n_layer
+    out = {
+        "metric": "GPT training step throughput (tokens/s), 12L d768 H12 Co-ALiBi, B8 S1024",
+        "value": round(batch * seq / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (uniform-random token ids), random-init weights",
+        "config": {"workload": "GPT training step (fwd+bwd+AdamW), BASELINE configs[4]", "layers": cfg.n_layer,
+                   "d_model": cfg.d_model, "heads": cfg.n_head, "vocab": cfg.vocab, "global_batch": batch,
+                   "seq_len": seq, "params": model.n_params()},
+        "final_loss": round(loss.item(), 4),
+        "attention_ms_per_step": round(attn_ms, 3),
+        "attention_share": round(attn_ms / ms, 3),
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
               "(the Co-ALiBi op is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "gpt":
+        gpt_bench(args)
+        return
 
     import torch
 
@@ -179,6 +243,31 @@ def main():
     traffic = read_traffic(os.path.join(ROOT, "profiles", f"traffic_{w.name}.md")).get(dominant)
     print(f"[bench] per-kernel: {json.dumps(per_kernel)}", file=sys.stderr, flush=True)
 
+    sdpa_ms = None
+    if args.sdpa and w.heads_q == w.heads_kv:
+        # Plain causal attention at the same shape and dtype (torch SDPA on ROCm), fwd + bwd:
+        # the cost of Co-ALiBi relative to ordinary attention.
+        import torch.nn.functional as F
+
+        qs, ks, vs = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+
+        def sdpa_step():
+            qs.grad = ks.grad = vs.grad = None
+            F.scaled_dot_product_attention(qs, ks, vs, is_causal=w.causal).backward(do)
+
+        for _ in range(3):
+            sdpa_step()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.steps):
+            sdpa_step()
+        end.record()
+        torch.cuda.synchronize()
+        sdpa_ms = start.elapsed_time(end) / args.steps
+        del qs, ks, vs
+        print(f"[bench] torch SDPA causal fwd+bwd: {sdpa_ms:.3f} ms/step", file=sys.stderr, flush=True)
+
+
     out = {
         "metric": "fwd and bwd TFLOPS (and % of MFMA peak) at B4 H16 S4096 D128 fp16 causal",
         "value": round(value, 2),
@@ -203,6 +292,8 @@ def main():
         "ref_convention_tflops": {"fwd": round(2 * fwd_flops / (fwd_ms * 1e-3) / 1e12, 2),
                                   "bwd": round(4 * fwd_flops / (bwd_ms * 1e-3) / 1e12, 2)},
         "kernels": per_kernel,
+        "sdpa_ms_per_step": None if sdpa_ms is None else round(sdpa_ms, 4),
+        "coalibi_over_sdpa": None if sdpa_ms is None else round(ms_step / sdpa_ms, 3),
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),
                      "traffic": None if traffic is None else round(traffic)},
