@@ -156,6 +156,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_bwd_dq_ke
 
   vec8 qf[C::KS], dof[C::KS];
   float dpart = 0.f;
+  const float tile_sc2 = sizeof(T) == 2 ? 1.0f : args.sc2;  // Q carries the scale in 16-bit types
   {
     const T* __restrict__ Qr = static_cast<const T*>(args.q) + qoff + (size_t)row * D;
     const T* __restrict__ dOr = static_cast<const T*>(args.dout) + qoff + (size_t)row * D;
@@ -164,6 +165,8 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_bwd_dq_ke
     for (int ks = 0; ks < C::KS; ++ks) {
       const int c0 = ks * 16 + hh * 8;
       qf[ks] = row_ok ? ld_vec8(Qr + c0) : zero_vec8<T>();
+      // 16-bit types: Q pre-scaled by sm_scale*log2(e), as in the forward.
+      if constexpr (sizeof(T) == 2) qf[ks] = scale_vec8<T>(qf[ks], args.sc2);
       dof[ks] = row_ok ? ld_vec8(dOr + c0) : zero_vec8<T>();
       const vec8 of = row_ok ? ld_vec8(Or + c0) : zero_vec8<T>();
 #pragma unroll
@@ -213,10 +216,10 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_bwd_dq_ke
     vec8 sb[2], pb[2];
     float atot;
     if (masked)
-      dp_tile<T, true, CAUSAL>(sacc, dacc, zb, crun, lse2, dsum, k0 + hh * 16, row, hh, Skv, Sq, args.sc2, lam,
+      dp_tile<T, true, CAUSAL>(sacc, dacc, zb, crun, lse2, dsum, k0 + hh * 16, row, hh, Skv, Sq, tile_sc2, lam,
                                lam2, sb, pb, atot);
     else
-      dp_tile<T, false, CAUSAL>(sacc, dacc, zb, crun, lse2, dsum, k0 + hh * 16, row, hh, Skv, Sq, args.sc2,
+      dp_tile<T, false, CAUSAL>(sacc, dacc, zb, crun, lse2, dsum, k0 + hh * 16, row, hh, Skv, Sq, tile_sc2,
                                 lam, lam2, sb, pb, atot);
     if (hh == 0 && row_ok) cb_row[(size_t)kt * Sq] = crun;
     crun += atot;

@@ -112,6 +112,16 @@ __device__ __forceinline__ typename Mfma<T>::vec8 ld_vec8(const T* p) {
   return *reinterpret_cast<const typename Mfma<T>::vec8*>(p);
 }
 
+// x * s, rounded back to T once per element.  The 16-bit kernels fold sm_scale*log2(e)
+// into the Q fragments with this, so S^T comes out of the MFMA already in log2 units.
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::vec8 scale_vec8(typename Mfma<T>::vec8 x, float s) {
+  f32x8 f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = static_cast<float>(x[e]) * s;
+  return Mfma<T>::pack(f);
+}
+
 template <typename T>
 __device__ __forceinline__ typename Mfma<T>::vec8 zero_vec8() {
   typename Mfma<T>::vec8 z;

@@ -192,10 +192,16 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
   const int row = wrow0 + col;
   const bool row_ok = row < Sq;
 
+  // 16-bit types: Q pre-scaled by sm_scale*log2(e) (one rounding per element, far below the
+  // input precision's effect on q.k), so the tile math takes the scale 1 and multiplies by nothing.
+  constexpr bool kPreScaled = sizeof(T) == 2;
   vec8 qf[C::KS];
 #pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks)
+  for (int ks = 0; ks < C::KS; ++ks) {
     qf[ks] = row_ok ? ld_vec8(Qp + (size_t)row * D + ks * 16 + hh * 8) : zero_vec8<T>();
+    if constexpr (kPreScaled) qf[ks] = scale_vec8<T>(qf[ks], sc2);
+  }
+  const float tile_sc2 = kPreScaled ? 1.0f : sc2;
 
   const int last_key = CAUSAL ? min(q0 + kFwdBM - 1, Skv - 1) : Skv - 1;
   const int nkt = last_key / kFwdBN + 1;
@@ -228,10 +234,10 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
     const bool masked = (CAUSAL && k0 + kFwdBN - 1 > wrow0) || (k0 + kFwdBN > Skv);
     float zst0, zst1;
     if (masked)
-      fwd_tile<T, D, CAUSAL, true>(sK, sV, qf, acc, m2, lsum, zr, zst0, zst1, k0, row, lane, Skv, sc2,
+      fwd_tile<T, D, CAUSAL, true>(sK, sV, qf, acc, m2, lsum, zr, zst0, zst1, k0, row, lane, Skv, tile_sc2,
                                    lam2);
     else
-      fwd_tile<T, D, CAUSAL, false>(sK, sV, qf, acc, m2, lsum, zr, zst0, zst1, k0, row, lane, Skv, sc2,
+      fwd_tile<T, D, CAUSAL, false>(sK, sV, qf, acc, m2, lsum, zr, zst0, zst1, k0, row, lane, Skv, tile_sc2,
                                     lam2);
     if (hh == 0 && row_ok) {
       zb_row[(size_t)(2 * kt) * Sq] = zst0;
