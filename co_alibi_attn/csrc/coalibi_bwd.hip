@@ -17,10 +17,12 @@
 // need no atomics and no per-query-block partial buffers:
 //   pass 1 (query-major, keys left to right): S^T, dS^T, dP, dQ^T += K^T dP^T.
 //     It writes D_i and cb[i][J] = sum over keys k < 32J of dA_ik.
-//   pass 2 (key-major, one work-group per 128 keys of a key head, 32 keys per
-//     wavefront): for every query head of the group and every query tile,
-//     S^T, dS^T, dP from the forward's zb and pass 1's cb, then
-//     dV^T += dO^T s and dK^T += Q^T dP.
+//   pass 2 (key-major, one work-group per 128 keys of a key head): for every
+//     query head of the group and every query tile, S^T, dS^T, dP from the
+//     forward's zb and pass 1's cb, then dV^T += dO^T s and dK^T += Q^T dP.
+//     fp16/bf16: 8 wavefronts, a pair per 32-key group that splits the query
+//     tile for S^T/dS^T/dP and the head dim for dV/dK; fp32: 4 wavefronts, one
+//     per 32-key group.
 // Both passes hold keys on the accumulator rows (each lane: 16 consecutive keys
 // of one query), so both key scans stay in registers.  z inside a 32-key block
 // is zb[i][J] minus the exclusive prefix of sigma in the block, so no long
