@@ -17,12 +17,12 @@
 // need no atomics and no per-query-block partial buffers:
 //   pass 1 (query-major, keys left to right): S^T, dS^T, dP, dQ^T += K^T dP^T.
 //     It writes D_i and cb[i][J] = sum over keys k < 32J of dA_ik.
-//   pass 2 (key-major, one work-group per 128 keys of a key head): for every
+//   pass 2 (key-major, one work-group per block of keys of a key head): for every
 //     query head of the group and every query tile, S^T, dS^T, dP from the
 //     forward's zb and pass 1's cb, then dV^T += dO^T s and dK^T += Q^T dP.
-//     fp16/bf16: 8 wavefronts, a pair per 32-key group that splits the query
-//     tile for S^T/dS^T/dP and the head dim for dV/dK; fp32: 4 wavefronts, one
-//     per 32-key group.
+//     fp16/bf16: 64 keys per work-group, a wavefront pair per 32-key group that
+//     splits the query tile for S^T/dS^T/dP and the head dim for dV/dK; fp32:
+//     128 keys, one wavefront per 32-key group.
 // Both passes hold keys on the accumulator rows (each lane: 16 consecutive keys
 // of one query), so both key scans stay in registers.  z inside a 32-key block
 // is zb[i][J] minus the exclusive prefix of sigma in the block, so no long
@@ -454,25 +454,27 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
 }
 
 
-// Pass 2 for fp16/bf16: dK, dV with wavefront pairs.  A work-group of 8
-// wavefronts owns 128 keys in four key groups kg of 32 and walks query tiles of 64
-// rows.  Wavefront (kg, qh) holds K and V of its key group as MFMA A operands (as
-// above) and computes S^T, dS^T and then s, dP for query half qh of the tile into
-// its key group's LDS buffer.  After a barrier each wavefront of the pair reduces
-// over all 64 queries of the tile, but only for its half of the head dim:
+// Pass 2 for fp16/bf16: dK, dV with wavefront pairs.  A work-group of 4
+// wavefronts owns 64 keys in two key groups kg of 32 and walks query tiles of 64
+// rows.  Wavefront (kg, qh) holds K of its key group as MFMA A operands (as
+// above; V comes from LDS) and computes S^T, dS^T and then s, dP for query half qh
+// of the tile into its key group's LDS buffer.  After a barrier each wavefront of
+// the pair reduces over all 64 queries of the tile, but only for its half of the
+// head dim:
 //   dV^T[d][key] += dO^T[d][q] s[q][key],  dK^T[d][key] += Q^T[d][q] dP[q][key],
 // for d in [qh*D/2, qh*D/2 + D/2).  Splitting the accumulators and the score tile
-// this way halves the registers of the one-wavefront-per-key-group form, which
-// gives two wavefronts per SIMD at no extra elementwise work.  Q and dO tiles
-// arrive by buffer-to-LDS DMA into a second buffer while the current tile is in
-// use, so no registers hold the next tile; K stays in registers and V is read from
-// LDS (both in full would not fit the register budget at D = 128).
-constexpr int kPairBK = 128;    // keys per work-group
+// this way halves the registers of the one-wavefront-per-key-group form, so two
+// work-groups share a CU (two wavefronts per SIMD from independent work-groups,
+// whose barriers do not align their phases) at no extra elementwise work.  The
+// next Q and dO tiles arrive by buffer-to-LDS DMA issued once the current tile is
+// no longer read; the other work-group on the CU covers that latency.
+constexpr int kPairBK = 64;     // keys per work-group
 constexpr int kPairBQ = 64;     // query rows per tile
-constexpr int kPairWaves = 8;   // wavefronts per work-group: 4 key groups x 2 query halves
+constexpr int kPairWaves = 4;   // wavefronts per work-group: 2 key groups x 2 query halves
+// Two work-groups per CU: 77 KB of LDS and at most 256 VGPRs each.
 
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(BwdArgs args) {
+__global__ __launch_bounds__(64 * kPairWaves, 2) void coalibi_bwd_dkdv_kernel(BwdArgs args) {
   static_assert(sizeof(T) == 2, "the wavefront-pair pass 2 is the 16-bit path");
   using C = BwdCfg<T, D>;
   using M = Mfma<T>;
@@ -486,8 +488,8 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(Bw
   constexpr int DMA_SLOTS = (NDMA + kPairWaves - 1) / kPairWaves;
   static_assert(BQ * CPR % 64 == 0, "tile must split into whole DMA instructions");
   constexpr int LDSP = 32 + C::CH;  // s / dP rows: 32 keys + one 16-byte pad
-  __shared__ __align__(16) T sQ[2][TILE];
-  __shared__ __align__(16) T sdO[2][TILE];
+  __shared__ __align__(16) T sQ[1][TILE];   // one buffer: the next tile lands after this one is read
+  __shared__ __align__(16) T sdO[1][TILE];
   __shared__ __align__(16) T sV[kPairBK * C::LDR];       // V rows, permuted per 32-key group
   __shared__ __align__(16) T sSP[NKG][2][BQ * LDSP];     // per key group: s and dP, [q][key]
   __shared__ __align__(16) float sLse2[2][BQ];
@@ -511,12 +513,12 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(Bw
   T* __restrict__ sS = sSP[kg][0];
   T* __restrict__ sP = sSP[kg][1];
 
-  // Zero both tile buffers once: DMA slots past the last query row then hold zeros.
+  // Zero the tile buffers once: DMA slots past the last query row then hold zeros.
   {
     u32x4* z = reinterpret_cast<u32x4*>(&sQ[0][0]);
-    for (int i = tid; i < 2 * TILE * (int)sizeof(T) / 16; i += 64 * kPairWaves) z[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = tid; i < TILE * (int)sizeof(T) / 16; i += 64 * kPairWaves) z[i] = u32x4{0u, 0u, 0u, 0u};
     z = reinterpret_cast<u32x4*>(&sdO[0][0]);
-    for (int i = tid; i < 2 * TILE * (int)sizeof(T) / 16; i += 64 * kPairWaves) z[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = tid; i < TILE * (int)sizeof(T) / 16; i += 64 * kPairWaves) z[i] = u32x4{0u, 0u, 0u, 0u};
   }
 
   vec8 ka[C::KS];
@@ -611,21 +613,18 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(Bw
 
   int gi = 0, qt = qt0;  // current work item; the next one is (gn, qn)
   for (int w = 0; w < nwork; ++w) {
-    const int buf = w & 1;
+    const int buf = w & 1;  // statistics buffer
     const bool wrap = qt + 1 == nQT;
     const int gn = wrap ? gi + 1 : gi, qn = wrap ? qt0 : qt + 1;
     const int hq = hkv * group + gi;
     const float lam = args.slopes[hq];
     const float lam2 = lam * kLog2e;
     const int q0 = qt * BQ;
-    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's DMA of tile w (and stats of tile w+1 issued last round)
-    __syncthreads();                // every wavefront's DMA landed; tile w-1 is no longer read
-    if (w + 1 < nwork) {
-      issue_tile(gn, qn, buf ^ 1);
-      load_stats(gn, qn);
-    }
-    const T* __restrict__ tQ = sQ[buf];
-    const T* __restrict__ tdO = sdO[buf];
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's DMA of tile w
+    __syncthreads();                // every wavefront's DMA of tile w landed
+    if (w + 1 < nwork) load_stats(gn, qn);
+    const T* __restrict__ tQ = sQ[0];
+    const T* __restrict__ tdO = sdO[0];
 
     // Query half h of the tile meets this key group (some pair is visible).
     auto half_live = [&](int h) {
@@ -678,7 +677,11 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void coalibi_bwd_dkdv_kernel(Bw
     }
     // Statistics of tile w+1 (loaded during this tile) into the other buffer; that
     // buffer was last read in tile w-1.
-    if (w + 1 < nwork) store_stats(buf ^ 1);
+    if (w + 1 < nwork) {
+      store_stats(buf ^ 1);
+      __syncthreads();  // tile w and the score buffers are no longer read
+      issue_tile(gn, qn, 0);
+    }
     gi = gn;
     qt = qn;
   }
