@@ -483,10 +483,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 2) void coalibi_bwd_dkdv_kernel(Bw
   constexpr int NKG = kPairBK / 32;
   constexpr int DH = C::DT / 2;                   // 32-row tiles of d per wavefront
   constexpr int TILE = BQ * C::LDR;               // elements of one padded Q or dO tile
-  constexpr int CPR = C::LDR * (int)sizeof(T) / 16;  // 16-byte chunks per padded LDS row
-  constexpr int NDMA = BQ * CPR / 64;             // wavefront DMA instructions per tile
-  constexpr int DMA_SLOTS = (NDMA + kPairWaves - 1) / kPairWaves;
-  static_assert(BQ * CPR % 64 == 0, "tile must split into whole DMA instructions");
+  using Dma = DmaTile<T, D, BQ, C::LDR, kPairWaves, false>;
   constexpr int LDSP = 32 + C::CH;  // s / dP rows: 32 keys + one 16-byte pad
   __shared__ __align__(16) T sQ[1][TILE];   // one buffer: the next tile lands after this one is read
   __shared__ __align__(16) T sdO[1][TILE];
@@ -514,12 +511,8 @@ __global__ __launch_bounds__(64 * kPairWaves, 2) void coalibi_bwd_dkdv_kernel(Bw
   T* __restrict__ sP = sSP[kg][1];
 
   // Zero the tile buffers once: DMA slots past the last query row then hold zeros.
-  {
-    u32x4* z = reinterpret_cast<u32x4*>(&sQ[0][0]);
-    for (int i = tid; i < TILE * (int)sizeof(T) / 16; i += 64 * kPairWaves) z[i] = u32x4{0u, 0u, 0u, 0u};
-    z = reinterpret_cast<u32x4*>(&sdO[0][0]);
-    for (int i = tid; i < TILE * (int)sizeof(T) / 16; i += 64 * kPairWaves) z[i] = u32x4{0u, 0u, 0u, 0u};
-  }
+  lds_zero(&sQ[0][0], (int)sizeof(sQ), tid, 64 * kPairWaves);
+  lds_zero(&sdO[0][0], (int)sizeof(sdO), tid, 64 * kPairWaves);
 
   vec8 ka[C::KS];
   {
@@ -549,16 +542,8 @@ __global__ __launch_bounds__(64 * kPairWaves, 2) void coalibi_bwd_dkdv_kernel(Bw
     dv[i] = f32x16{};
   }
 
-  // DMA source offsets of this lane for its instruction slots: slot m is tile chunk
-  // c = (wave + 8m)*64 + lane, i.e. padded row c / CPR, chunk c % CPR; pad chunks
-  // point past the resource and read as zero.
-  int dma_off[DMA_SLOTS];
-#pragma unroll
-  for (int m = 0; m < DMA_SLOTS; ++m) {
-    const int c = (wave + kPairWaves * m) * 64 + lane;
-    const int row = c / CPR, j = c - row * CPR;
-    dma_off[m] = j < D / 8 ? (row * D + j * 8) * (int)sizeof(T) : 0x40000000;
-  }
+  Dma dma;  // the Q and dO tiles share the chunk layout
+  dma.init(wave, lane);
 
   // Work list: (query head gi, query tile qt) pairs.
   const int nQT = (Sq + BQ - 1) / BQ;
@@ -567,18 +552,9 @@ __global__ __launch_bounds__(64 * kPairWaves, 2) void coalibi_bwd_dkdv_kernel(Bw
   const int nwork = per_head * group;
   const int jb = kw0 / 32;  // this key group's 32-key block
   auto issue_tile = [&](int gi, int qt, int buf) {
-    const size_t qoff = ((size_t)(b * args.Hq + hkv * group + gi) * Sq + (size_t)qt * BQ) * D;
-    const int elems = min(max(Sq - qt * BQ, 0), BQ) * D;
-    const __amdgpu_buffer_rsrc_t rq = tile_rsrc(static_cast<const T*>(args.q) + qoff, elems);
-    const __amdgpu_buffer_rsrc_t rd = tile_rsrc(static_cast<const T*>(args.dout) + qoff, elems);
-#pragma unroll
-    for (int m = 0; m < DMA_SLOTS; ++m) {
-      const int i = wave + kPairWaves * m;
-      if (i < NDMA) {
-        dma16_to_lds(rq, &sQ[buf][i * 64 * 16 / (int)sizeof(T)], dma_off[m]);
-        dma16_to_lds(rd, &sdO[buf][i * 64 * 16 / (int)sizeof(T)], dma_off[m]);
-      }
-    }
+    const size_t qoff = (size_t)(b * args.Hq + hkv * group + gi) * Sq * D;
+    dma.issue(static_cast<const T*>(args.q) + qoff, qt * BQ, Sq, sQ[buf], wave);
+    dma.issue(static_cast<const T*>(args.dout) + qoff, qt * BQ, Sq, sdO[buf], wave);
   };
   // Per-row statistics of a tile, one value per lane (= tile row) through buffer
   // loads (rows past Sq and blocks past the last read as zero): wavefront 0 loads

@@ -149,6 +149,48 @@ namespace coalibi {
 
 template <typename T, int N> struct VecOf { typedef T type __attribute__((ext_vector_type(N))); };
 
+// A ROWS x D tile of a row-major [nrows][D] matrix staged into an LDS tile of row
+// stride LD (elements, padded) by buffer-to-LDS DMA.  One DMA instruction writes 64
+// consecutive 16-byte chunks, so the padded tile is a run of ROWS*LD*sizeof(T)/16
+// chunks split over the work-group's NWAVES wavefronts; each lane keeps the source
+// offset of its chunk in every instruction slot it issues (tile-invariant).  Pad
+// chunks and rows at or beyond `nrows` point past the buffer resource and land as
+// zeros.  PERM: LDS row R of every 32-row block holds source row kRowOfReg(R), the
+// order in which an A operand with keys on the accumulator rows reads them.
+template <typename T, int D, int ROWS, int LD, int NWAVES, bool PERM>
+struct DmaTile {
+  static constexpr int CPR = LD * (int)sizeof(T) / 16;  // chunks per padded LDS row
+  static constexpr int NINSTR = ROWS * CPR / 64;         // wavefront DMA instructions per tile
+  static constexpr int SLOTS = (NINSTR + NWAVES - 1) / NWAVES;
+  static_assert(LD * (int)sizeof(T) % 16 == 0 && ROWS * CPR % 64 == 0, "tile must split into DMA instructions");
+  static_assert(!PERM || ROWS % 32 == 0, "rows are permuted in blocks of 32");
+  int off[SLOTS];
+
+  __device__ __forceinline__ void init(int wave, int lane) {
+#pragma unroll
+    for (int m = 0; m < SLOTS; ++m) {
+      const int c = (wave + NWAVES * m) * 64 + lane;
+      const int r = c / CPR, j = c - r * CPR;
+      const int src = PERM ? (r & ~31) + kRowOfReg(r & 31) : r;
+      off[m] = j < D / 8 ? (src * D + j * 8) * (int)sizeof(T) : 0x40000000;
+    }
+  }
+  __device__ __forceinline__ void issue(const T* base, int row0, int nrows, T* lds, int wave) const {
+    const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(base + (size_t)row0 * D, min(max(nrows - row0, 0), ROWS) * D);
+#pragma unroll
+    for (int m = 0; m < SLOTS; ++m) {
+      const int i = wave + NWAVES * m;
+      if (i < NINSTR) dma16_to_lds(rsrc, lds + i * 64 * 16 / (int)sizeof(T), off[m]);
+    }
+  }
+};
+
+// Zero `bytes` (a multiple of 16) of LDS with the whole work-group of `nthreads`.
+__device__ __forceinline__ void lds_zero(void* p, int bytes, int tid, int nthreads) {
+  u32x4* z = reinterpret_cast<u32x4*>(p);
+  for (int i = tid; i < bytes / 16; i += nthreads) z[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
 // Stages a ROWS x D tile of a row-major [rows][D] matrix through registers into
 // LDS, 16 bytes per load/store.  Rows at or beyond `nrows` read as zero.
 //   GROUPED = false: consecutive threads own consecutive 16-byte chunks of a row
