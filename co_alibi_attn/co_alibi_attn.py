@@ -47,6 +47,50 @@ def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def _forward(q, k, v, slopes, causal, sm_scale, with_stats: bool):
+    """Checks (as the reference's co_alibi_attn.py:30-33) and the native forward.
+
+    Returns (o, lse, zb); with ``with_stats=False`` (inference) lse and zb are
+    None and the kernel writes neither.
+    """
+    batch_size, num_heads, seq_len_q, head_dim = q.shape
+    num_kv_heads, seq_len_kv = k.shape[1], k.shape[2]
+
+    assert num_kv_heads >= 1 and num_heads % num_kv_heads == 0
+    assert k.shape == (batch_size, num_kv_heads, seq_len_kv, head_dim)
+    assert v.shape == (batch_size, num_kv_heads, seq_len_kv, head_dim)
+    assert q.is_cuda and k.is_cuda and v.is_cuda, "Inputs must be CUDA tensors"
+    assert slopes.shape == (num_heads,), f"Slopes shape {slopes.shape} doesn't match num_heads {num_heads}"
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _native.DTYPE_CODES:
+        raise TypeError(f"q, k, v must share one dtype of float32/float16/bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
+    if head_dim not in _native.SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {_native.SUPPORTED_HEAD_DIMS}, got {head_dim}")
+
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    slopes32 = slopes.detach().to(device=q.device, dtype=torch.float32).contiguous()
+    o = torch.empty_like(q)
+    lib = _native.lib()
+    lse = zb = None
+    if with_stats:
+        lse = torch.empty((batch_size, num_heads, seq_len_q), device=q.device, dtype=torch.float32)
+        zb = torch.empty(
+            lib.co_alibi_zb_numel(batch_size, num_heads, seq_len_q, seq_len_kv),
+            device=q.device,
+            dtype=torch.float32,
+        )
+    with torch.cuda.device(q.device):
+        _native.check(
+            lib.co_alibi_fwd(
+                _native.DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                slopes32.data_ptr(), o.data_ptr(), 0 if lse is None else lse.data_ptr(),
+                0 if zb is None else zb.data_ptr(),
+                batch_size, num_heads, num_kv_heads, seq_len_q, seq_len_kv, head_dim,
+                1 if causal else 0, float(sm_scale), _stream_handle(q.device),
+            )
+        )
+    return o, lse, zb, (q, k, v, slopes32)
+
+
 class CoALIBIAttention(torch.autograd.Function):
     """Autograd function over the native forward / backward (reference co_alibi_attn.py:24-135).
 
@@ -57,38 +101,7 @@ class CoALIBIAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, slopes, causal, sm_scale):
-        batch_size, num_heads, seq_len_q, head_dim = q.shape
-        num_kv_heads, seq_len_kv = k.shape[1], k.shape[2]
-
-        assert num_kv_heads >= 1 and num_heads % num_kv_heads == 0
-        assert k.shape == (batch_size, num_kv_heads, seq_len_kv, head_dim)
-        assert v.shape == (batch_size, num_kv_heads, seq_len_kv, head_dim)
-        assert q.is_cuda and k.is_cuda and v.is_cuda, "Inputs must be CUDA tensors"
-        assert slopes.shape == (num_heads,), f"Slopes shape {slopes.shape} doesn't match num_heads {num_heads}"
-        if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _native.DTYPE_CODES:
-            raise TypeError(f"q, k, v must share one dtype of float32/float16/bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
-        if head_dim not in _native.SUPPORTED_HEAD_DIMS:
-            raise ValueError(f"head_dim must be one of {_native.SUPPORTED_HEAD_DIMS}, got {head_dim}")
-
-        q, k, v = _aligned(q), _aligned(k), _aligned(v)
-        slopes32 = slopes.detach().to(device=q.device, dtype=torch.float32).contiguous()
-        o = torch.empty_like(q)
-        lse = torch.empty((batch_size, num_heads, seq_len_q), device=q.device, dtype=torch.float32)
-        lib = _native.lib()
-        zb = torch.empty(
-            lib.co_alibi_zb_numel(batch_size, num_heads, seq_len_q, seq_len_kv),
-            device=q.device,
-            dtype=torch.float32,
-        )
-        with torch.cuda.device(q.device):
-            _native.check(
-                lib.co_alibi_fwd(
-                    _native.DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                    slopes32.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(),
-                    batch_size, num_heads, num_kv_heads, seq_len_q, seq_len_kv, head_dim,
-                    1 if causal else 0, float(sm_scale), _stream_handle(q.device),
-                )
-            )
+        o, lse, zb, (q, k, v, slopes32) = _forward(q, k, v, slopes, causal, sm_scale, with_stats=True)
         ctx.save_for_backward(q, k, v, o, lse, zb, slopes32)
         ctx.sm_scale = sm_scale
         ctx.causal = causal
@@ -126,10 +139,16 @@ def co_alibi_attention(q, k, v, causal=True, sm_scale=None, bias_max=8.0):
     head h uses key/value head h // (Hq // Hkv).  Returns (B, Hq, Sq, D) in
     q.dtype.  ``sm_scale`` defaults to D**-0.5; the per-head slope is twice the
     ALiBi slope of ``_get_coalibi_slopes(Hq, bias_max)``, rounded to q.dtype.
+    When no gradient can flow (grad mode off, or no input requires grad) the
+    forward runs without saving anything for a backward.
     """
     if sm_scale is None:
         sm_scale = 1.0 / (q.shape[-1] ** 0.5)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     num_q_heads = q.shape[1]
     slopes = (2.0 * _get_coalibi_slopes(num_q_heads, bias_max)).to(q.device, dtype=q.dtype)
+    if not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)):
+        # Inference: no autograd record, and the statistics only the backward reads
+        # (LSE and the penalty block sums) are neither allocated nor written.
+        return _forward(q, k, v, slopes, causal, sm_scale, with_stats=False)[0]
     return CoALIBIAttention.apply(q, k, v, slopes, causal, sm_scale)

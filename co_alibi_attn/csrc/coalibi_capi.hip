@@ -44,6 +44,13 @@ int check_shape(const char* fn, int dtype, const Shape& s) {
   return CO_ALIBI_OK;
 }
 
+// Optional outputs may be NULL; when given they must be aligned.
+int check_opt_ptr(const char* fn, const char* name, const void* p, uintptr_t align) {
+  if (p != nullptr && !aligned(p, align))
+    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": " + name + " is not " + std::to_string(align) + "-byte aligned");
+  return CO_ALIBI_OK;
+}
+
 int check_ptr(const char* fn, const char* name, const void* p, uintptr_t align) {
   if (p == nullptr) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": " + name + " is NULL");
   if (!aligned(p, align))
@@ -96,7 +103,7 @@ int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const f
   if ((rc = check_shape(fn, dtype, s))) return rc;
   if ((rc = check_ptr(fn, "q", q, 16)) || (rc = check_ptr(fn, "k", k, 16)) || (rc = check_ptr(fn, "v", v, 16)) ||
       (rc = check_ptr(fn, "o", o, 16)) || (rc = check_ptr(fn, "slopes", slopes, 4)) ||
-      (rc = check_ptr(fn, "lse", lse, 4)) || (rc = check_ptr(fn, "zb", zb, 4)))
+      (rc = check_opt_ptr(fn, "lse", lse, 4)) || (rc = check_opt_ptr(fn, "zb", zb, 4)))
     return rc;
   if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, "co_alibi_fwd: sm_scale must be finite");
 

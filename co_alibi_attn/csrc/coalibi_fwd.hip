@@ -215,7 +215,9 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
   float m2 = kNegInf, lsum = 0.f, zr = 0.f;
-  float* __restrict__ zb_row = args.zb + (size_t)bh * args.nZB * Sq + row;
+  // Inference callers pass no zb / lse: the statistics only the backward reads are skipped.
+  const bool write_zb = args.zb != nullptr;
+  float* __restrict__ zb_row = write_zb ? args.zb + (size_t)bh * args.nZB * Sq + row : nullptr;
 
   for (int kt = nkt - 1; kt >= 0; --kt) {
     __syncthreads();
@@ -239,7 +241,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
     else
       fwd_tile<T, D, CAUSAL, false>(sK, sV, qf, acc, m2, lsum, zr, zst0, zst1, k0, row, lane, Skv, tile_sc2,
                                     lam2);
-    if (hh == 0 && row_ok) {
+    if (write_zb && hh == 0 && row_ok) {
       zb_row[(size_t)(2 * kt) * Sq] = zst0;
       if (k0 + 32 < Skv) zb_row[(size_t)(2 * kt + 1) * Sq] = zst1;
     }
@@ -262,7 +264,8 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
         *reinterpret_cast<vec4*>(Orow + dt * 32 + g * 8 + hh * 4) = __builtin_convertvector(v4, vec4);
       }
     }
-    if (hh == 0) args.lse[(size_t)bh * Sq + row] = ltot > 0.f ? (m2 + log2f(ltot)) * kLn2 : kNegInf;
+    if (hh == 0 && args.lse != nullptr)
+      args.lse[(size_t)bh * Sq + row] = ltot > 0.f ? (m2 + log2f(ltot)) * kLn2 : kNegInf;
   }
 }
 

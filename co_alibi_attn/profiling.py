@@ -82,7 +82,12 @@ class KernelSet:
                                                 p(self.zb), p(self.lam), p(self.dk), p(self.dv), p(self.ws),
                                                 self.ws_bytes, *shape))
 
+        def fwd_inference():  # no LSE / zb: the forward of a caller that needs no backward
+            _native.check(lib.co_alibi_fwd(code, p(self.q), p(self.k), p(self.v), p(self.lam), p(self.o), 0, 0,
+                                           *shape))
+
         self.launch = dict(zip(KERNELS, (fwd, dq, dkdv)))
+        self.launch["coalibi_fwd_kernel (inference)"] = fwd_inference
         pairs = S * S / 2.0 if w.causal else float(S * S)
         self.gemm_flops = 2.0 * B * Hq * D * pairs
 

@@ -54,7 +54,8 @@ size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_k
 /* Forward: writes o (B,Hq,Sq,D, dtype), lse (B,Hq,Sq, fp32 natural log-sum-exp
  * m_i + log(l_i), co_alibi_fwd_kernel.py:120) and zb.  The reference adds 1e-9
  * to l_i there and in the O normaliser (:115); l_i >= 1 here, so that term is
- * below fp32 resolution and is left out. */
+ * below fp32 resolution and is left out.  lse and zb may be NULL (inference: the
+ * statistics only co_alibi_bwd reads are then not written); o is the same. */
 int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const float* slopes,
                  void* o, float* lse, float* zb, int batch, int heads_q, int heads_kv, int seq_q,
                  int seq_kv, int head_dim, int causal, float sm_scale, void* stream);

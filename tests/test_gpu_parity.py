@@ -173,6 +173,30 @@ def test_repeat_call_deterministic():
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["fp16", "bf16", "fp32"])
+def test_inference_forward_equals_training_forward(dtype):
+    """Without gradients the forward writes no LSE / zb and returns bit-identical O
+    (drop-in API under no_grad, with inputs that need no grad, and the C ABI with NULL)."""
+    lib = _native.lib()
+    for B, Hq, Hkv, Sq, Skv, D, causal in [(1, 4, 2, 200, 200, 64, True), (1, 2, 2, 70, 190, 128, False)]:
+        q, k, v, _ = rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=9)
+        qd, kd, vd = (t.to(DEV) for t in (q, k, v))
+        o_train = co_alibi_attention(qd.clone().requires_grad_(), kd, vd, causal=causal)
+        assert o_train.grad_fn is not None
+        with torch.no_grad():
+            o_nograd = co_alibi_attention(qd.clone().requires_grad_(), kd, vd, causal=causal)
+        o_plain = co_alibi_attention(qd, kd, vd, causal=causal)
+        assert o_nograd.grad_fn is None and o_plain.grad_fn is None
+        assert torch.equal(o_train.detach(), o_nograd) and torch.equal(o_nograd, o_plain)
+        lam = ref.slopes(Hq, 8.0, dtype=dtype).float().to(DEV)  # the drop-in's slopes, kept alive
+        o_abi = torch.empty_like(qd)
+        _native.check(lib.co_alibi_fwd(_native.DTYPE_CODES[dtype], qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                       lam.data_ptr(), o_abi.data_ptr(), 0, 0, B, Hq, Hkv, Sq, Skv, D,
+                                       int(causal), 1.0 / math.sqrt(D), torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        assert torch.equal(o_abi, o_plain)
+
+
 def test_sm_scale_and_bias_max_arguments():
     q, k, v, do = rand_inputs(1, 3, 3, 120, 120, 64, torch.float32, seed=5)
     got = hip_fwd_bwd(q, k, v, do, causal=True, sm_scale=0.3, bias_max=4.0)
