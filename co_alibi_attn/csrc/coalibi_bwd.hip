@@ -694,7 +694,7 @@ hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream) {
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
-    if constexpr (sizeof(T) == 2) {
+    if constexpr (sizeof(T) == 2 && D >= 64) {  // the pair kernel splits D into 32-row halves
       const int nKB = (a.Skv + kPairBK - 1) / kPairBK;
       hipLaunchKernelGGL((coalibi_bwd_dkdv_kernel<T, D, CAUSAL>), dim3(nKB * a.B * a.Hkv), dim3(64 * kPairWaves),
                          0, stream, a);
@@ -713,10 +713,13 @@ hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream) {
   template hipError_t launch_bwd<T, D, true>(const BwdArgs&, int, hipStream_t); \
   template hipError_t launch_bwd<T, D, false>(const BwdArgs&, int, hipStream_t);
 
+COALIBI_INST_BWD(_Float16, 32)
 COALIBI_INST_BWD(_Float16, 64)
 COALIBI_INST_BWD(_Float16, 128)
+COALIBI_INST_BWD(__bf16, 32)
 COALIBI_INST_BWD(__bf16, 64)
 COALIBI_INST_BWD(__bf16, 128)
+COALIBI_INST_BWD(float, 32)
 COALIBI_INST_BWD(float, 64)
 COALIBI_INST_BWD(float, 128)
 

@@ -35,8 +35,9 @@ int check_shape(const char* fn, int dtype, const Shape& s) {
     return fail(CO_ALIBI_EINVAL, std::string(fn) + ": batch, heads and sequence lengths must be >= 1");
   if (s.Hq % s.Hkv != 0)
     return fail(CO_ALIBI_EINVAL, std::string(fn) + ": heads_q must be a multiple of heads_kv");
-  if (s.D != 64 && s.D != 128)
-    return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": head_dim must be 64 or 128, got " + std::to_string(s.D));
+  if (s.D != 32 && s.D != 64 && s.D != 128)
+    return fail(CO_ALIBI_EUNSUPPORTED,
+                std::string(fn) + ": head_dim must be 32, 64 or 128, got " + std::to_string(s.D));
   // Sequence indices are 32-bit in the kernels; grids must fit a 31-bit launch.
   const double wg = std::ceil(s.Sq / 128.0) * s.B * s.Hq;
   if (s.Sq > (1 << 30) || s.Skv > (1 << 30) || wg > 2147483647.0)
@@ -65,7 +66,11 @@ hipError_t fwd_dispatch_causal(const coalibi::FwdArgs& a, bool causal, hipStream
 
 template <typename T>
 hipError_t fwd_dispatch_d(const coalibi::FwdArgs& a, int D, bool causal, hipStream_t st) {
-  return D == 64 ? fwd_dispatch_causal<T, 64>(a, causal, st) : fwd_dispatch_causal<T, 128>(a, causal, st);
+  switch (D) {
+    case 32: return fwd_dispatch_causal<T, 32>(a, causal, st);
+    case 64: return fwd_dispatch_causal<T, 64>(a, causal, st);
+    default: return fwd_dispatch_causal<T, 128>(a, causal, st);
+  }
 }
 
 template <typename T, int D>
@@ -75,8 +80,11 @@ hipError_t bwd_dispatch_causal(const coalibi::BwdArgs& a, bool causal, int stage
 
 template <typename T>
 hipError_t bwd_dispatch_d(const coalibi::BwdArgs& a, int D, bool causal, int stages, hipStream_t st) {
-  return D == 64 ? bwd_dispatch_causal<T, 64>(a, causal, stages, st)
-                 : bwd_dispatch_causal<T, 128>(a, causal, stages, st);
+  switch (D) {
+    case 32: return bwd_dispatch_causal<T, 32>(a, causal, stages, st);
+    case 64: return bwd_dispatch_causal<T, 64>(a, causal, stages, st);
+    default: return bwd_dispatch_causal<T, 128>(a, causal, stages, st);
+  }
 }
 
 }  // namespace

@@ -209,8 +209,9 @@ struct TileLoader {
   static constexpr int KG = !GROUPED ? 1
                             : ((ROWS / 4) * CPR >= 256) ? 4 : ((ROWS / 2) * CPR >= 256) ? 2 : 1;
   static constexpr int NG = (ROWS / KG) * CPR;  // groups per tile
-  static constexpr int GPT = NG / 256;          // groups per thread
-  static_assert(NG % 256 == 0 && GPT >= 1, "tile does not split over 256 threads");
+  static constexpr int GPT = (NG + 255) / 256;  // groups per thread
+  static constexpr bool kPartial = NG % 256 != 0;  // small tiles: threads >= NG idle
+  static_assert(NG < 256 || NG % 256 == 0, "tile does not split over 256 threads");
   static_assert(ROWS % 32 == 0, "rows are permuted in blocks of 32");
 
   u32x4 r[GPT][KG];
@@ -226,6 +227,7 @@ struct TileLoader {
 #pragma unroll
     for (int i = 0; i < GPT; ++i) {
       const int g = tid + 256 * i;
+      if (kPartial && g >= NG) continue;
       const int rr = grp_row(g), cc = grp_col(g);
 #pragma unroll
       for (int k = 0; k < KG; ++k)
@@ -238,6 +240,7 @@ struct TileLoader {
 #pragma unroll
     for (int i = 0; i < GPT; ++i) {
       const int g = tid + 256 * i;
+      if (kPartial && g >= NG) continue;
       const int rr = grp_row(g), cc = grp_col(g);
 #pragma unroll
       for (int k = 0; k < KG; ++k) {
@@ -256,6 +259,7 @@ struct TileLoader {
 #pragma unroll
     for (int i = 0; i < GPT; ++i) {
       const int g = tid + 256 * i;
+      if (kPartial && g >= NG) continue;
       const int rr = grp_row(g), cc = grp_col(g);
       chunk rows[KG];
 #pragma unroll

@@ -283,10 +283,13 @@ hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
   template hipError_t launch_fwd<T, D, true>(const FwdArgs&, hipStream_t); \
   template hipError_t launch_fwd<T, D, false>(const FwdArgs&, hipStream_t);
 
+COALIBI_INST_FWD(_Float16, 32)
 COALIBI_INST_FWD(_Float16, 64)
 COALIBI_INST_FWD(_Float16, 128)
+COALIBI_INST_FWD(__bf16, 32)
 COALIBI_INST_FWD(__bf16, 64)
 COALIBI_INST_FWD(__bf16, 128)
+COALIBI_INST_FWD(float, 32)
 COALIBI_INST_FWD(float, 64)
 COALIBI_INST_FWD(float, 128)
 

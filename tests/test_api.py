@@ -53,7 +53,7 @@ def _fwd(lib, **over):
     (dict(q=None), 1, "q is NULL"),
     (dict(k=24), 1, "k is not 16-byte aligned"),
     (dict(lse=2), 1, "lse is not 4-byte aligned"),
-    (dict(D=96), 2, "head_dim must be 64 or 128"),
+    (dict(D=96), 2, "head_dim must be 32, 64 or 128"),
     (dict(dtype=7), 2, "dtype must be"),
     (dict(Hq=3, Hkv=2), 1, "multiple of heads_kv"),
     (dict(Sq=0), 1, ">= 1"),

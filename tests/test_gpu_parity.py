@@ -95,6 +95,8 @@ CASES = [
     (1, 2, 2, 100, 100, 64, False),     # non-causal
     (1, 4, 2, 70, 190, 128, False),     # non-causal, rectangular, grouped
     (1, 2, 2, 300, 300, 64, True),      # several key tiles, partial last tile
+    (1, 4, 2, 150, 150, 32, True),      # head dim 32, grouped heads
+    (1, 2, 2, 90, 200, 32, False),      # head dim 32, non-causal, rectangular
 ]
 
 
