@@ -3,7 +3,8 @@
 Same public surface as the reference module co_alibi_attn/co_alibi_attn.py:
 ``co_alibi_attention(q, k, v, causal=True, sm_scale=None, bias_max=8.0)``
 (reference :137-148), the autograd function ``CoALIBIAttention`` (:24-135) and
-the slope helper ``_get_coalibi_slopes`` (:11-22).  The work runs in the
+the slope helper ``_get_coalibi_slopes`` (:11-22), plus ``co_alibi_decode``, a
+split-K decode step over a key / value cache that the reference lacks.  The work runs in the
 hand-written gfx950 kernels of ``libco_alibi.so`` (C ABI in include/co_alibi.h);
 grouped-query attention is handled inside the kernels instead of by
 ``repeat_interleave``.
@@ -14,7 +15,7 @@ import torch
 
 from . import _native
 
-__all__ = ["co_alibi_attention", "CoALIBIAttention", "_get_coalibi_slopes"]
+__all__ = ["co_alibi_attention", "co_alibi_decode", "CoALIBIAttention", "_get_coalibi_slopes"]
 
 
 def _get_coalibi_slopes(n_heads: int, bias_max: float = 8.0) -> torch.Tensor:
@@ -152,3 +153,56 @@ def co_alibi_attention(q, k, v, causal=True, sm_scale=None, bias_max=8.0):
         # (LSE and the penalty block sums) are neither allocated nor written.
         return _forward(q, k, v, slopes, causal, sm_scale, with_stats=False)[0]
     return CoALIBIAttention.apply(q, k, v, slopes, causal, sm_scale)
+
+
+def co_alibi_decode(q, k_cache, v_cache, seq_len=None, sm_scale=None, bias_max=8.0, return_lse=False):
+    """One decode step: the newest query of every head against a key / value cache.
+
+    q: (B, Hq, 1, D); k_cache, v_cache: (B, Hkv, capacity, D) with the first
+    ``seq_len`` rows (default: all) of every head filled.  All of them are visible
+    to the query, so the result equals ``co_alibi_attention(q, k_cache[:, :, :seq_len],
+    v_cache[:, :, :seq_len], causal=False, sm_scale, bias_max)`` (reference
+    co_alibi_attn.py:137-148; its top-left causal mask would let an Sq = 1 query see
+    only the first key).  Inference only: no autograd record.  Returns o (B, Hq, 1, D)
+    in q.dtype, and with ``return_lse`` also the natural-log LSE (B, Hq, 1) in fp32.
+    """
+    if q.dim() != 4 or q.shape[2] != 1:
+        raise ValueError(f"q must be (B, Hq, 1, D), got {tuple(q.shape)}")
+    batch_size, num_heads, _, head_dim = q.shape
+    num_kv_heads, capacity = k_cache.shape[1], k_cache.shape[2]
+    if seq_len is None:
+        seq_len = capacity
+    assert k_cache.shape == (batch_size, num_kv_heads, capacity, head_dim)
+    assert v_cache.shape == k_cache.shape
+    assert num_kv_heads >= 1 and num_heads % num_kv_heads == 0
+    assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "Inputs must be CUDA tensors"
+    if not 1 <= seq_len <= capacity:
+        raise ValueError(f"seq_len must be in [1, {capacity}], got {seq_len}")
+    if not (q.dtype == k_cache.dtype == v_cache.dtype) or q.dtype not in _native.DTYPE_CODES:
+        raise TypeError(
+            f"q and the caches must share one dtype of float32/float16/bfloat16, got "
+            f"{q.dtype}, {k_cache.dtype}, {v_cache.dtype}"
+        )
+    if head_dim not in _native.SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {_native.SUPPORTED_HEAD_DIMS}, got {head_dim}")
+    if sm_scale is None:
+        sm_scale = 1.0 / (head_dim ** 0.5)
+
+    q, k_cache, v_cache = _aligned(q.detach()), _aligned(k_cache.detach()), _aligned(v_cache.detach())
+    slopes = (2.0 * _get_coalibi_slopes(num_heads, bias_max)).to(q.device, dtype=q.dtype)
+    slopes32 = slopes.to(torch.float32).contiguous()
+    o = torch.empty_like(q)
+    lse = torch.empty((batch_size, num_heads, 1), device=q.device, dtype=torch.float32) if return_lse else None
+    lib = _native.lib()
+    ws_bytes = lib.co_alibi_decode_workspace_bytes(batch_size, num_heads, seq_len, head_dim)
+    workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        _native.check(
+            lib.co_alibi_decode(
+                _native.DTYPE_CODES[q.dtype], q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                slopes32.data_ptr(), o.data_ptr(), 0 if lse is None else lse.data_ptr(),
+                workspace.data_ptr(), ws_bytes, batch_size, num_heads, num_kv_heads, seq_len, capacity,
+                head_dim, float(sm_scale), _stream_handle(q.device),
+            )
+        )
+    return (o, lse) if return_lse else o

@@ -1,6 +1,8 @@
 // C ABI entry points: argument checks, dtype / head-dim dispatch, launches.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -228,6 +230,110 @@ int co_alibi_bwd_dkdv(int dtype, const void* dout, const void* q, const void* k,
   return bwd_impl("co_alibi_bwd_dkdv", 2, dtype, dout, q, k, v, nullptr, lse, zb, slopes, nullptr, dk, dv,
                   workspace, workspace_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal,
                   sm_scale, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+template <typename T>
+hipError_t decode_dispatch_d(const coalibi::DecodeArgs& a, int D, hipStream_t st) {
+  switch (D) {
+    case 32: return coalibi::launch_decode<T, 32>(a, st);
+    case 64: return coalibi::launch_decode<T, 64>(a, st);
+    default: return coalibi::launch_decode<T, 128>(a, st);
+  }
+}
+
+size_t decode_chunks(int seq_kv) {
+  return (static_cast<size_t>(seq_kv) + coalibi::kDecodeChunkKeys - 1) / coalibi::kDecodeChunkKeys;
+}
+
+// Compute units of the current device (queried once per device).
+int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t co_alibi_decode_workspace_bytes(int batch, int heads_q, int seq_kv, int head_dim) {
+  if (batch < 1 || heads_q < 1 || seq_kv < 1 || head_dim < 1) return 0;
+  const size_t parts = static_cast<size_t>(batch) * heads_q * decode_chunks(seq_kv);
+  return 3 * round_up(parts * sizeof(float), 256) + parts * head_dim * sizeof(float);
+}
+
+int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v_cache, const float* slopes,
+                    void* o, float* lse, void* workspace, size_t workspace_bytes, int batch, int heads_q,
+                    int heads_kv, int seq_kv, int kv_capacity, int head_dim, float sm_scale, void* stream) {
+  const char* fn = "co_alibi_decode";
+  const Shape s{batch, heads_q, heads_kv, 1, seq_kv, head_dim};
+  int rc;
+  if ((rc = check_shape(fn, dtype, s))) return rc;
+  if (heads_q / heads_kv > coalibi::kMaxDecodeGroup)
+    return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": at most " + std::to_string(coalibi::kMaxDecodeGroup) +
+                                           " query heads per kv head");
+  if (kv_capacity < seq_kv) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": kv_capacity is below seq_kv");
+  if (decode_chunks(seq_kv) > static_cast<size_t>(coalibi::kMaxDecodeChunks))
+    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": seq_kv above " +
+                                     std::to_string(coalibi::kMaxDecodeChunks * coalibi::kDecodeChunkKeys));
+  if ((rc = check_ptr(fn, "q", q, 16)) || (rc = check_ptr(fn, "k_cache", k_cache, 16)) ||
+      (rc = check_ptr(fn, "v_cache", v_cache, 16)) || (rc = check_ptr(fn, "o", o, 16)) ||
+      (rc = check_ptr(fn, "slopes", slopes, 4)) || (rc = check_opt_ptr(fn, "lse", lse, 4)) ||
+      (rc = check_ptr(fn, "workspace", workspace, 256)))
+    return rc;
+  const size_t need = co_alibi_decode_workspace_bytes(batch, heads_q, seq_kv, head_dim);
+  if (workspace_bytes < need)
+    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": workspace of " + std::to_string(workspace_bytes) +
+                                     " bytes, need " + std::to_string(need));
+  if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": sm_scale must be finite");
+
+  const size_t parts = static_cast<size_t>(batch) * heads_q * decode_chunks(seq_kv);
+  const size_t stat_bytes = round_up(parts * sizeof(float), 256);
+  char* ws = static_cast<char*>(workspace);
+  coalibi::DecodeArgs a{};
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.slopes = slopes;
+  a.o = o;
+  a.lse = lse;
+  a.pmax = reinterpret_cast<float*>(ws);
+  a.psum = reinterpret_cast<float*>(ws + stat_bytes);
+  a.psig = reinterpret_cast<float*>(ws + 2 * stat_bytes);
+  a.pout = reinterpret_cast<float*>(ws + 3 * stat_bytes);
+  a.B = batch;
+  a.Hq = heads_q;
+  a.Hkv = heads_kv;
+  a.G = heads_q / heads_kv;
+  a.L = seq_kv;
+  a.cap = kv_capacity;
+  a.nChunks = static_cast<int>(decode_chunks(seq_kv));
+  // Enough splits to give every CU kDecodeWGsPerCU work-groups; each walks cps chunks.
+  const long long units = static_cast<long long>(batch) * heads_kv;
+  const long long want = (static_cast<long long>(coalibi::kDecodeWGsPerCU) * device_cus() + units - 1) / units;
+  const int splits = static_cast<int>(std::max(1LL, std::min<long long>(want, a.nChunks)));
+  a.cps = (a.nChunks + splits - 1) / splits;
+  a.nSplits = (a.nChunks + a.cps - 1) / a.cps;
+  a.sc2 = sm_scale * coalibi::kLog2eHost;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (dtype) {
+    case CO_ALIBI_F16: e = decode_dispatch_d<_Float16>(a, head_dim, st); break;
+    case CO_ALIBI_BF16: e = decode_dispatch_d<__bf16>(a, head_dim, st); break;
+    default: e = decode_dispatch_d<float>(a, head_dim, st); break;
+  }
+  if (e != hipSuccess) return fail(CO_ALIBI_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return CO_ALIBI_OK;
 }
 
 const char* co_alibi_last_error(void) { return g_last_error.c_str(); }

@@ -159,6 +159,7 @@ template <typename T, int N> struct VecOf { typedef T type __attribute__((ext_ve
 // order in which an A operand with keys on the accumulator rows reads them.
 template <typename T, int D, int ROWS, int LD, int NWAVES, bool PERM>
 struct DmaTile {
+  static constexpr int CH = 16 / (int)sizeof(T);        // elements per 16-byte chunk
   static constexpr int CPR = LD * (int)sizeof(T) / 16;  // chunks per padded LDS row
   static constexpr int NINSTR = ROWS * CPR / 64;         // wavefront DMA instructions per tile
   static constexpr int SLOTS = (NINSTR + NWAVES - 1) / NWAVES;
@@ -172,7 +173,7 @@ struct DmaTile {
       const int c = (wave + NWAVES * m) * 64 + lane;
       const int r = c / CPR, j = c - r * CPR;
       const int src = PERM ? (r & ~31) + kRowOfReg(r & 31) : r;
-      off[m] = j < D / 8 ? (src * D + j * 8) * (int)sizeof(T) : 0x40000000;
+      off[m] = j < D / CH ? (src * D + j * CH) * (int)sizeof(T) : 0x40000000;
     }
   }
   __device__ __forceinline__ void issue(const T* base, int row0, int nrows, T* lds, int wave) const {

@@ -45,8 +45,37 @@ struct BwdArgs {
   float sm_scale;
 };
 
+// Decode: q/o (B, Hq, D); the caches k/v are (B, Hkv, cap, D) with the first L rows
+// of every head valid.  The keys form nChunks chunks of kDecodeChunkKeys; split s of a
+// head covers chunks [s*cps, (s+1)*cps).  Split-K partials per (b*Hq + h, split):
+// pmax / psum / psig (B*Hq, nSplits) and pout (B*Hq, nSplits, D), fp32.
+constexpr int kDecodeChunkKeys = 256;
+constexpr int kMaxDecodeGroup = 32;     // query heads per kv head (MFMA tile columns)
+constexpr int kMaxDecodeChunks = 8192;  // chunk weights held in LDS by the merge
+
+struct DecodeArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* slopes;  // (Hq,)
+  void* o;
+  float* lse;  // (B*Hq,) or NULL
+  float* pmax;
+  float* psum;
+  float* psig;
+  float* pout;
+  int B, Hq, Hkv, G, L, cap, nChunks, cps, nSplits;
+  float sc2;
+};
+
+// Split-K work-groups the decode aims at per CU (two are resident at a time).
+constexpr int kDecodeWGsPerCU = 4;
+
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
+
+template <typename T, int D>
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
 
 // stages: bit 0 = pass 1 (dq, dsum, cb), bit 1 = pass 2 (dk, dv; needs pass 1's dsum / cb).
 template <typename T, int D, bool CAUSAL>

@@ -115,6 +115,55 @@ class KernelSet:
         return e0.elapsed_time(e1) / reps
 
 
+class DecodeSet:
+    """Device buffers of one decode workload and its C-ABI launcher (split + merge kernels)."""
+
+    KERNELS = ("coalibi_decode_split_kernel", "coalibi_decode_merge_kernel")
+
+    def __init__(self, w, device="cuda:0", seed: int = 0):
+        import torch
+
+        from co_alibi_attn import _native
+        from co_alibi_attn.co_alibi_attn import _get_coalibi_slopes
+        from co_alibi_attn.workloads import make_decode_inputs
+
+        self.w = w
+        dev = torch.device(device)
+        lib = _native.lib()
+        B, Hq, Hkv, L, D = w.batch, w.heads_q, w.heads_kv, w.seq_kv, w.head_dim
+        self.q, self.k, self.v = make_decode_inputs(w, seed=seed, device=dev)
+        self.lam = (2.0 * _get_coalibi_slopes(Hq, w.bias_max)).to(w.dtype).float().to(dev)
+        self.o = torch.empty_like(self.q)
+        self.lse = torch.empty(B, Hq, device=dev, dtype=torch.float32)
+        self.ws_bytes = lib.co_alibi_decode_workspace_bytes(B, Hq, L, D)
+        self.ws = torch.empty(self.ws_bytes, device=dev, dtype=torch.uint8)
+        self.stream = torch.cuda.current_stream(dev)
+        code = _native.DTYPE_CODES[w.dtype]
+        p = lambda t: t.data_ptr()  # noqa: E731
+        args = (code, p(self.q), p(self.k), p(self.v), p(self.lam), p(self.o), p(self.lse), p(self.ws),
+                self.ws_bytes, B, Hq, Hkv, L, L, D, 1.0 / math.sqrt(D), self.stream.cuda_stream)
+
+        def step():
+            _native.check(lib.co_alibi_decode(*args))
+
+        self.step = step
+        elem = self.q.element_size()
+        # Algorithmic HBM bytes of one step: the cache rows, q and o.
+        self.bytes = w.cache_bytes() + 2 * B * Hq * D * elem
+
+    def time(self, reps: int) -> float:
+        """Average step duration in ms over ``reps`` back-to-back steps, HIP events on the launch stream."""
+        import torch
+
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        for _ in range(reps):
+            self.step()
+        e1.record(self.stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+
 def calibration_copy(device="cuda:0", nbytes: int = CALIBRATION_BYTES) -> None:
     """A device-to-device copy of ``nbytes``: it reads and writes exactly ``nbytes`` of HBM."""
     import torch

@@ -56,3 +56,41 @@ def make_inputs(w: Workload, seed: int = 0, device: str | torch.device = "cpu", 
         v = torch.randn(B, w.heads_kv, S, w.head_dim, generator=gen) * w.v_scale
     do = torch.randn(B, w.heads_q, S, w.head_dim, generator=gen)
     return tuple(t.to(w.dtype).to(device) for t in (q, k, v, do))
+
+
+@dataclass(frozen=True)
+class DecodeWorkload:
+    """One decode step: a query per (batch, query head) against caches of ``seq_kv`` filled rows."""
+
+    name: str
+    batch: int
+    heads_q: int
+    heads_kv: int
+    seq_kv: int
+    head_dim: int
+    dtype: torch.dtype
+    bias_max: float = 8.0
+    scale: float = 0.5  # q, k, v ~ scale * N(0, 1)
+
+    def cache_bytes(self) -> int:
+        """Bytes of the K and V rows one step reads."""
+        return 2 * self.batch * self.heads_kv * self.seq_kv * self.head_dim * torch.finfo(self.dtype).bits // 8
+
+
+DECODE_WORKLOADS = {
+    # The next token after a prefill of BASELINE configs[2] (grouped-query, 8192 positions).
+    "decode_gqa": DecodeWorkload("decode_gqa", 1, 32, 8, 8192, 128, torch.bfloat16),
+    # The same model serving 16 sequences at once.
+    "decode_serving": DecodeWorkload("decode_serving", 16, 32, 8, 8192, 128, torch.bfloat16),
+    # One long-context sequence.
+    "decode_long": DecodeWorkload("decode_long", 1, 32, 8, 131072, 128, torch.bfloat16),
+}
+
+
+def make_decode_inputs(w: DecodeWorkload, seed: int = 0, device: str | torch.device = "cpu"):
+    """(q (B,Hq,1,D), k_cache, v_cache (B,Hkv,seq_kv,D)) of decode workload ``w``, in w.dtype."""
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(w.batch, w.heads_q, 1, w.head_dim, generator=gen) * w.scale
+    k = torch.randn(w.batch, w.heads_kv, w.seq_kv, w.head_dim, generator=gen) * w.scale
+    v = torch.randn(w.batch, w.heads_kv, w.seq_kv, w.head_dim, generator=gen) * w.scale
+    return tuple(t.to(w.dtype).to(device) for t in (q, k, v))

@@ -86,6 +86,25 @@ int co_alibi_bwd_dkdv(int dtype, const void* dout, const void* q, const void* k,
                       void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv,
                       int seq_q, int seq_kv, int head_dim, int causal, float sm_scale, void* stream);
 
+/* Bytes of device scratch co_alibi_decode needs: the split-K partials, 4 + head_dim
+ * fp32 per (batch, query head, 256-key chunk). */
+size_t co_alibi_decode_workspace_bytes(int batch, int heads_q, int seq_kv, int head_dim);
+
+/* Decode: one new query per (batch, query head) against a key / value cache.
+ * q and o are (B, Hq, D); k_cache and v_cache are (B, Hkv, kv_capacity, D) with the
+ * first seq_kv rows of every head valid, all of them visible to the query (the
+ * newest position).  lse (B*Hq fp32, natural log) may be NULL.  The reference has
+ * no decode entry point: this is its forward, co_alibi_attention(q, k, v,
+ * causal=False) (co_alibi_attn/co_alibi_attn.py:137-148), with Sq = 1 and the
+ * caches cut to seq_kv rows; its top-left causal mask (co_alibi_fwd_kernel.py:80-90)
+ * would show an Sq = 1 query only the first key.  At most 32 query heads per kv
+ * head, seq_kv <= 2^21; workspace holds co_alibi_decode_workspace_bytes(...) bytes
+ * (256-byte aligned). */
+int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v_cache,
+                    const float* slopes, void* o, float* lse, void* workspace,
+                    size_t workspace_bytes, int batch, int heads_q, int heads_kv, int seq_kv,
+                    int kv_capacity, int head_dim, float sm_scale, void* stream);
+
 /* Message describing the last failed call on this thread ("" if none). */
 const char* co_alibi_last_error(void);
 

@@ -78,7 +78,8 @@ def test_bwd_argument_errors():
 
 
 def test_public_surface_matches_reference():
-    assert co_alibi_attn.__all__ == ["co_alibi_attention"]
+    # the reference package exports exactly co_alibi_attention; the decode step is an addition
+    assert co_alibi_attn.__all__ == ["co_alibi_attention", "co_alibi_decode"]
     import inspect
     sig = inspect.signature(co_alibi_attn.co_alibi_attention)
     assert list(sig.parameters) == ["q", "k", "v", "causal", "sm_scale", "bias_max"]
@@ -107,3 +108,51 @@ def test_slopes_dtype_rounding():
     # 2^(0.5 - h/2): odd h are exact powers of two, even h round in fp16
     assert s16[1].item() == 1.0 and s16[15].item() == 2.0 ** -7
     assert abs(s16[0].item() - 2 ** 0.5) < 2 ** 0.5 * 2 ** -11
+
+
+def test_decode_sizes():
+    lib = _native.lib()
+    # 256-key chunks; per (b, h, chunk): max, sum, sigma total (each array 256-byte padded) + D floats
+    parts = 2 * 32 * 64  # B=2, Hq=32, 16384 keys
+    assert lib.co_alibi_decode_workspace_bytes(2, 32, 16384, 128) == 3 * parts * 4 + parts * 128 * 4
+    assert lib.co_alibi_decode_workspace_bytes(1, 1, 257, 64) == 3 * 256 + 2 * 64 * 4
+    assert lib.co_alibi_decode_workspace_bytes(1, 1, 0, 64) == 0
+
+
+def _decode(lib, **over):
+    args = dict(dtype=1, q=256, k=256, v=256, slopes=256, o=256, lse=None, ws=256, ws_bytes=1 << 20, B=1, Hq=8,
+                Hkv=2, L=300, cap=512, D=128, scale=0.125)
+    args.update(over)
+    return lib.co_alibi_decode(args["dtype"], args["q"], args["k"], args["v"], args["slopes"], args["o"],
+                               args["lse"], args["ws"], args["ws_bytes"], args["B"], args["Hq"], args["Hkv"],
+                               args["L"], args["cap"], args["D"], args["scale"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(k=None), 1, "k_cache is NULL"),
+    (dict(v=8), 1, "v_cache is not 16-byte aligned"),
+    (dict(ws=16), 1, "workspace is not 256-byte aligned"),
+    (dict(ws_bytes=1000), 1, "workspace of 1000 bytes"),
+    (dict(cap=299), 1, "kv_capacity is below seq_kv"),
+    (dict(L=(1 << 21) + 1, cap=1 << 22), 1, "seq_kv above 2097152"),
+    (dict(Hq=66, Hkv=1), 2, "at most 32 query heads per kv head"),
+    (dict(Hq=6, Hkv=4), 1, "multiple of heads_kv"),
+    (dict(D=80), 2, "head_dim must be 32, 64 or 128"),
+    (dict(L=0), 1, ">= 1"),
+    (dict(scale=float("inf")), 1, "sm_scale must be finite"),
+])
+def test_decode_argument_errors(over, code, msg):
+    lib = _native.lib()
+    assert _decode(lib, **over) == code
+    assert msg in lib.co_alibi_last_error().decode()
+
+
+def test_decode_python_checks():
+    q = torch.randn(1, 4, 2, 64)
+    kc = torch.randn(1, 2, 16, 64)
+    with pytest.raises(ValueError, match=r"\(B, Hq, 1, D\)"):
+        co_alibi_attn.co_alibi_decode(q, kc, kc)
+    with pytest.raises(AssertionError, match="CUDA"):
+        co_alibi_attn.co_alibi_decode(q[:, :, :1], kc, kc)
+    with pytest.raises(AssertionError):
+        co_alibi_attn.co_alibi_decode(q[:, :, :1], kc, kc[:, :, :8])
