@@ -13,7 +13,10 @@ Also measured in the same run:
     launch that the rocprofv3 FETCH_SIZE/WRITE_SIZE passes recorded in
     profiles/traffic_<workload>.md (null when that file is absent);
   * the CPU baseline: the repository's CPU restatement of model.py (oracle,
-    fp32) on a time-bounded sample of the same workload.
+    fp32) on a time-bounded sample of the same workload;
+  * decode steps (``co_alibi_decode``: one query per head against a key/value
+    cache) of the decode workloads, against the HBM roofline: algorithmic bytes
+    are the cache rows read plus q and o.
 """
 from __future__ import annotations
 
@@ -46,6 +49,8 @@ def parse_args():
     ap.add_argument("--kernel-rounds", type=int, default=5, help="rounds of the per-kernel timing (median reported)")
     ap.add_argument("--no-sdpa", dest="sdpa", action="store_false",
                     help="skip the torch SDPA (plain causal attention) comparison")
+    ap.add_argument("--no-decode", dest="decode", action="store_false",
+                    help="skip the decode-step measurement (co_alibi_decode over a key/value cache)")
     return ap.parse_args()
 
 
@@ -172,6 +177,32 @@ def gpt_bench(args) -> None:
         "attention_share": round(attn_ms / ms, 3),
     }
     print(json.dumps(out), flush=True)
+
+
+def decode_bench(args):
+    """Decode steps (split + merge kernels through the C ABI) of every decode workload: HBM roofline."""
+    import torch
+
+    from co_alibi_attn.profiling import DecodeSet
+    from co_alibi_attn.workloads import DECODE_WORKLOADS
+
+    out = {}
+    for name, w in DECODE_WORKLOADS.items():
+        ds = DecodeSet(w)
+        ds.step()
+        torch.cuda.synchronize()
+        ds.time(10)
+        ms = sorted(ds.time(max(args.kernel_reps, 20)) for _ in range(args.kernel_rounds))[args.kernel_rounds // 2]
+        gbs = ds.bytes / (ms * 1e-3) / 1e9
+        out[name] = {"config": {"batch": w.batch, "heads_q": w.heads_q, "heads_kv": w.heads_kv, "seq_kv": w.seq_kv,
+                                "head_dim": w.head_dim, "dtype": str(w.dtype).split(".")[-1]},
+                     "us_per_step": round(ms * 1e3, 2), "bytes_per_step": ds.bytes,
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+        print(f"[bench] decode {name}: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+        del ds
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -308,6 +339,8 @@ def main():
                      "frac": round(achieved / peak, 4),
                      "traffic": None if traffic is None else round(traffic)},
     }
+    if args.decode:
+        out["decode"] = decode_bench(args)
     if args.cpu_seconds > 0:
         print("[bench] CPU baseline ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)

@@ -8,6 +8,8 @@ benchmark:
   python3 co_alibi_attn/profiling.py run --workload headline --reps 3
       one 1 GiB device-to-device copy (the HBM-counter calibration: it reads
       and writes exactly 1 GiB), then each kernel ``reps`` times, nothing else
+      (a decode workload, e.g. ``--workload decode_serving``, runs ``reps``
+      decode steps instead: the split and the merge kernel)
   python3 co_alibi_attn/profiling.py stats DIR --command CMD --out FILE
       per-kernel duration table from ``rocprofv3 --kernel-trace --stats``
   python3 co_alibi_attn/profiling.py traffic FETCH_DIR WRITE_DIR --command CMD --out FILE
@@ -37,6 +39,8 @@ if __package__ in (None, ""):
 
 CALIBRATION_BYTES = 1 << 30
 KERNELS = ("coalibi_fwd_kernel", "coalibi_bwd_dq_kernel", "coalibi_bwd_dkdv_kernel")
+DECODE_KERNELS = ("coalibi_decode_split_kernel", "coalibi_decode_merge_kernel")
+NAMED_KERNELS = KERNELS + DECODE_KERNELS
 # (charged, issued) products per launch, in units of one GEMM of 2*B*Hq*D flops per visible pair.
 PRODUCTS = {"coalibi_fwd_kernel": (2, 2), "coalibi_bwd_dq_kernel": (1, 3), "coalibi_bwd_dkdv_kernel": (4, 4)}
 
@@ -118,7 +122,7 @@ class KernelSet:
 class DecodeSet:
     """Device buffers of one decode workload and its C-ABI launcher (split + merge kernels)."""
 
-    KERNELS = ("coalibi_decode_split_kernel", "coalibi_decode_merge_kernel")
+    KERNELS = DECODE_KERNELS
 
     def __init__(self, w, device="cuda:0", seed: int = 0):
         import torch
@@ -178,9 +182,16 @@ def calibration_copy(device="cuda:0", nbytes: int = CALIBRATION_BYTES) -> None:
 def cmd_run(args) -> None:
     import torch
 
-    from co_alibi_attn.workloads import WORKLOADS
+    from co_alibi_attn.workloads import DECODE_WORKLOADS, WORKLOADS
 
     calibration_copy()
+    if args.workload in DECODE_WORKLOADS:
+        ds = DecodeSet(DECODE_WORKLOADS[args.workload])
+        for _ in range(args.reps):
+            ds.step()
+        torch.cuda.synchronize()
+        print(f"profiling run: {args.workload}, {args.reps} decode steps ({', '.join(DECODE_KERNELS)})", flush=True)
+        return
     ks = KernelSet(WORKLOADS[args.workload])
     for _ in range(args.reps):
         ks.prime()
@@ -200,7 +211,7 @@ def _csv_rows(directory: str, suffix: str):
 
 
 def _short(name: str) -> str:
-    for k in KERNELS:
+    for k in NAMED_KERNELS:
         if k in name:
             return k
     return name if len(name) <= 60 else name[:57] + "..."
@@ -253,15 +264,15 @@ def cmd_traffic(args) -> None:
         lines.append(f"- `{counter}`: calibration copy read {cal_kib:.0f} KiB, factor {factor:.4f}")
         for name, vals in per.items():
             k = _short(name)
-            if k in KERNELS:
+            if k in NAMED_KERNELS:
                 result.setdefault(k, {})[counter] = sum(vals) / len(vals) * 1024.0 * factor
     lines += ["", "| kernel | fetched (MB) | written (MB) | HBM traffic (MB) |", "|---|---:|---:|---:|"]
-    for k in KERNELS:
+    for k in NAMED_KERNELS:
         if k in result:
             f, wr = result[k].get("FETCH_SIZE", 0.0), result[k].get("WRITE_SIZE", 0.0)
             lines.append(f"| `{k}` | {f / 1e6:.1f} | {wr / 1e6:.1f} | {(f + wr) / 1e6:.1f} |")
     lines += ["", "Machine-readable (bytes per launch, read by bench.py):", ""]
-    for k in KERNELS:
+    for k in NAMED_KERNELS:
         if k in result:
             total = result[k].get("FETCH_SIZE", 0.0) + result[k].get("WRITE_SIZE", 0.0)
             lines.append(f"    traffic_bytes_per_launch {k} {total:.0f}")
