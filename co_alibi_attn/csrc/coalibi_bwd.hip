@@ -62,14 +62,17 @@ __device__ __forceinline__ bool pair_ok(int key, int row, int Skv, int Sq, bool 
 }
 
 // Elementwise core shared by both passes for one 32-key x 32-query tile held as
-// S^T (lane (col, hh): query q, keys hh*16 + r).  Inputs: sacc = q.k, dacc = dO.v,
-// zb = sum of sigma over keys >= the block start, cb = sum of dA over keys before
-// the block, lse2 = LSE*log2(e), dsum = dO.O.  Outputs the 16 values of s and dP
-// packed for the next products; returns the block's dA total in `atot_blk`.
+// S^T (lane (col, hh): query q, keys hh*16 + r).  Inputs: sacc = q.k (times sc2 gives
+// log2 units; sc2 = 1 when an operand carries the scale), dacc = dO.v - D (the dS
+// accumulator starts at -D = -dO.O), zb = sum of sigma over keys >= the block start,
+// cb = sum of dA over keys before the block, lse2 = LSE*log2(e).  Outputs the 16
+// values of s and dP packed for the next products; returns the block's dA total in
+// `atot_blk`.  C is carried multiplied by the slope (lam*C), which makes
+// dP = dA - lam*sigma'*C one fma per key after sigma' = sigma - sigma^2.
 template <typename T, bool MASKED, bool CAUSAL>
 __device__ __forceinline__ void dp_tile(const f32x16& sacc, f32x16& dacc, float zb, float cb, float lse2,
-                                        float dsum, int key0, int row, int hh, int Skv, int Sq, float sc2,
-                                        float lam, float lam2, typename Mfma<T>::vec8 (&sb)[2],
+                                        int key0, int row, int hh, int Skv, int Sq, float sc2, float lam,
+                                        float lam2, typename Mfma<T>::vec8 (&sb)[2],
                                         typename Mfma<T>::vec8 (&pb)[2], float& atot_blk) {
   using M = Mfma<T>;
   // Phase 1: sigma and this run's sigma total.
@@ -94,16 +97,16 @@ __device__ __forceinline__ void dp_tile(const f32x16& sacc, f32x16& dacc, float 
     float s = fast_exp2(fmaf(lam2, pre, fmaf(sacc[r], sc2, -cst)));
     pre += sg[r];
     if (MASKED) s = pair_ok(key0 + r, row, Skv, Sq, CAUSAL) ? s : 0.f;
-    const float da = s * (dacc[r] - dsum);
+    const float da = s * dacc[r];
     dacc[r] = da;
     atot += da;
     sv[r >> 3][r & 7] = s;
   }
   sb[0] = M::pack(sv[0]);
   sb[1] = M::pack(sv[1]);
-  // C = cb + (dA of the other half's run if left of ours) + inclusive prefix.
+  // lam*C = lam*(cb + (dA of the other half's run if left of ours) + inclusive prefix).
   const float aoth = other_half(atot);
-  float c = cb + (hh ? aoth : 0.f);
+  float c = lam * (cb + (hh ? aoth : 0.f));
   atot_blk = hh ? atot + aoth : aoth + atot;  // same order in both halves
 #pragma unroll
   for (int mh = 0; mh < 2; ++mh) {
@@ -112,9 +115,9 @@ __device__ __forceinline__ void dp_tile(const f32x16& sacc, f32x16& dacc, float 
     for (int e = 0; e < 8; ++e) {
       const int r = mh * 8 + e;
       const float da = dacc[r];
-      c += da;
+      c = fmaf(lam, da, c);
       const float sgv = sg[r];
-      float dp = fmaf(-lam * fmaf(-sgv, sgv, sgv), c, da);
+      float dp = fmaf(fmaf(sgv, sgv, -sgv), c, da);  // da - sigma'*lam*C
       if (MASKED) dp = pair_ok(key0 + r, row, Skv, Sq, CAUSAL) ? dp : 0.f;
       pv[e] = dp;
     }
@@ -208,7 +211,9 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_bwd_dq_ke
     const float zb = row_ok ? zb_row[(size_t)kt * Sq] : 0.f;
     const bool masked = (CAUSAL && k0 + kBN - 1 > wrow0) || (k0 + kBN > Skv) || (wrow0 + 32 > Sq);
 
-    f32x16 sacc = f32x16{}, dacc = f32x16{};
+    f32x16 sacc = f32x16{}, dacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dacc[r] = -dsum;
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
       sacc = M::k16(ld_vec8(sK + col * C::LDR + ks * 16 + hh * 8), qf[ks], sacc);
@@ -218,11 +223,11 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_bwd_dq_ke
     vec8 sb[2], pb[2];
     float atot;
     if (masked)
-      dp_tile<T, true, CAUSAL>(sacc, dacc, zb, crun, lse2, dsum, k0 + hh * 16, row, hh, Skv, Sq, tile_sc2, lam,
-                               lam2, sb, pb, atot);
+      dp_tile<T, true, CAUSAL>(sacc, dacc, zb, crun, lse2, k0 + hh * 16, row, hh, Skv, Sq, tile_sc2, lam, lam2,
+                               sb, pb, atot);
     else
-      dp_tile<T, false, CAUSAL>(sacc, dacc, zb, crun, lse2, dsum, k0 + hh * 16, row, hh, Skv, Sq, tile_sc2,
-                                lam, lam2, sb, pb, atot);
+      dp_tile<T, false, CAUSAL>(sacc, dacc, zb, crun, lse2, k0 + hh * 16, row, hh, Skv, Sq, tile_sc2, lam, lam2,
+                                sb, pb, atot);
     if (hh == 0 && row_ok) cb_row[(size_t)kt * Sq] = crun;
     crun += atot;
     __builtin_amdgcn_sched_barrier(0);
@@ -305,9 +310,12 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
       ka[ks] = key_ok ? ld_vec8(Kr + ks * 16 + hh * 8) : zero_vec8<T>();
+      // 16-bit types: K pre-scaled by sm_scale*log2(e), so S^T comes out in log2 units.
+      if constexpr (sizeof(T) == 2) ka[ks] = scale_vec8<T>(ka[ks], args.sc2);
       va[ks] = key_ok ? ld_vec8(Vr + ks * 16 + hh * 8) : zero_vec8<T>();
     }
   }
+  const float tile_sc2 = sizeof(T) == 2 ? 1.0f : args.sc2;
 
   f32x16 dk[C::DT], dv[C::DT];
 #pragma unroll
@@ -373,7 +381,10 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
       const int ql = sq * 32 + col;  // tile-local query row of this lane
       const int row = qs0 + col;
 
-      f32x16 sacc = f32x16{}, dacc = f32x16{};
+      f32x16 sacc = f32x16{}, dacc;
+      const float dsum = sDsum[ql];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dacc[r] = -dsum;
 #pragma unroll
       for (int ks = 0; ks < C::KS; ++ks) {
         sacc = M::k16(ka[ks], ld_vec8(sQ + ql * C::LDR + ks * 16 + hh * 8), sacc);
@@ -383,11 +394,11 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
       vec8 sb[2], pb[2];
       float atot;
       if (masked)
-        dp_tile<T, true, CAUSAL>(sacc, dacc, sZb[wave][ql], sCb[wave][ql], sLse2[ql], sDsum[ql], key0, row, hh,
-                                 Skv, Sq, args.sc2, lam, lam2, sb, pb, atot);
+        dp_tile<T, true, CAUSAL>(sacc, dacc, sZb[wave][ql], sCb[wave][ql], sLse2[ql], key0, row, hh, Skv, Sq,
+                                 tile_sc2, lam, lam2, sb, pb, atot);
       else
-        dp_tile<T, false, CAUSAL>(sacc, dacc, sZb[wave][ql], sCb[wave][ql], sLse2[ql], sDsum[ql], key0, row, hh,
-                                  Skv, Sq, args.sc2, lam, lam2, sb, pb, atot);
+        dp_tile<T, false, CAUSAL>(sacc, dacc, sZb[wave][ql], sCb[wave][ql], sLse2[ql], key0, row, hh, Skv, Sq,
+                                  tile_sc2, lam, lam2, sb, pb, atot);
       // s and dP to this wavefront's scratch, then back as operands reduced over queries.
       if constexpr (C::kTr) {
         *reinterpret_cast<vec8*>(sS + col * C::LDSP + hh * 16) = sb[0];
@@ -519,8 +530,10 @@ __global__ __launch_bounds__(64 * kPairWaves, 2) void coalibi_bwd_dkdv_kernel(Bw
     const int key = kw0 + kRowOfReg(col);
     const bool key_ok = key < Skv;
     const T* __restrict__ Kr = static_cast<const T*>(args.k) + kvoff + (size_t)key * D;
+    // K pre-scaled by sm_scale*log2(e), so S^T comes out in log2 units.
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) ka[ks] = key_ok ? ld_vec8(Kr + ks * 16 + hh * 8) : zero_vec8<T>();
+    for (int ks = 0; ks < C::KS; ++ks)
+      ka[ks] = scale_vec8<T>(key_ok ? ld_vec8(Kr + ks * 16 + hh * 8) : zero_vec8<T>(), args.sc2);
   }
   // V rows of the work-group's keys; LDS row R of each 32-row group holds key
   // kRowOfReg(R) of the group, the A-operand order.
@@ -612,7 +625,10 @@ __global__ __launch_bounds__(64 * kPairWaves, 2) void coalibi_bwd_dkdv_kernel(Bw
       const bool masked = (CAUSAL && qs0 < kw0 + 31) || (qs0 + 32 > Sq) || (kw0 + 32 > Skv);
       const int ql = qh * 32 + col;  // tile-local query row of this lane
       const int row = qs0 + col;
-      f32x16 sacc = f32x16{}, dacc = f32x16{};
+      f32x16 sacc = f32x16{}, dacc;
+      const float dsum = sDsum[buf][ql];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dacc[r] = -dsum;
 #pragma unroll
       for (int ks = 0; ks < C::KS; ++ks) {
         sacc = M::k16(ka[ks], ld_vec8(tQ + ql * C::LDR + ks * 16 + hh * 8), sacc);
@@ -622,11 +638,11 @@ __global__ __launch_bounds__(64 * kPairWaves, 2) void coalibi_bwd_dkdv_kernel(Bw
       vec8 sb[2], pb[2];
       float atot;
       if (masked)
-        dp_tile<T, true, CAUSAL>(sacc, dacc, sZb[buf][kg][ql], sCb[buf][kg][ql], sLse2[buf][ql], sDsum[buf][ql],
-                                 key0, row, hh, Skv, Sq, args.sc2, lam, lam2, sb, pb, atot);
+        dp_tile<T, true, CAUSAL>(sacc, dacc, sZb[buf][kg][ql], sCb[buf][kg][ql], sLse2[buf][ql], key0, row, hh,
+                                 Skv, Sq, 1.0f, lam, lam2, sb, pb, atot);
       else
-        dp_tile<T, false, CAUSAL>(sacc, dacc, sZb[buf][kg][ql], sCb[buf][kg][ql], sLse2[buf][ql], sDsum[buf][ql],
-                                  key0, row, hh, Skv, Sq, args.sc2, lam, lam2, sb, pb, atot);
+        dp_tile<T, false, CAUSAL>(sacc, dacc, sZb[buf][kg][ql], sCb[buf][kg][ql], sLse2[buf][ql], key0, row, hh,
+                                  Skv, Sq, 1.0f, lam, lam2, sb, pb, atot);
       *reinterpret_cast<vec8*>(sS + ql * LDSP + hh * 16) = sb[0];
       *reinterpret_cast<vec8*>(sS + ql * LDSP + hh * 16 + 8) = sb[1];
       *reinterpret_cast<vec8*>(sP + ql * LDSP + hh * 16) = pb[0];
