@@ -75,27 +75,29 @@ __device__ __forceinline__ void dp_tile(const f32x16& sacc, f32x16& dacc, float 
                                         float lam2, typename Mfma<T>::vec8 (&sb)[2],
                                         typename Mfma<T>::vec8 (&pb)[2], float& atot_blk) {
   using M = Mfma<T>;
-  // Phase 1: sigma and this run's sigma total.
-  float sg[16];
+  // Phase 1: sigma, its running (exclusive) prefix over this run folded into
+  // e = t + lam2*prefix, and the run's sigma total.
+  float sg[16], ex[16];
   float tot = 0.f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    float s = sigmoid_log2(sacc[r] * sc2);
+    const float t = sacc[r] * sc2;
+    float s = sigmoid_log2(t);
     if (MASKED) s = pair_ok(key0 + r, row, Skv, Sq, CAUSAL) ? s : 0.f;
     sg[r] = s;
+    ex[r] = fmaf(lam2, tot, t);
     tot += s;
   }
-  // z = zb - (sigma of the other half's run if it is left of ours) - exclusive prefix.
+  // z = zb - (sigma of the other half's run if it is left of ours) - exclusive prefix, so
+  // log2 of s = t - lam2*z - lse2 = e - (lam2*zbase + lse2).
   const float oth = other_half(tot);
   const float zbase = zb - (hh ? oth : 0.f);
-  // log2 of s:  t - lam2*(zbase - pre) - lse2 = fma(lam2, pre, fma(q.k, sc2, -(lam2*zbase + lse2)))
   const float cst = fmaf(lam2, zbase, lse2);
-  float pre = 0.f, atot = 0.f;
+  float atot = 0.f;
   f32x8 sv[2];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    float s = fast_exp2(fmaf(lam2, pre, fmaf(sacc[r], sc2, -cst)));
-    pre += sg[r];
+    float s = fast_exp2(ex[r] - cst);
     if (MASKED) s = pair_ok(key0 + r, row, Skv, Sq, CAUSAL) ? s : 0.f;
     const float da = s * dacc[r];
     dacc[r] = da;
