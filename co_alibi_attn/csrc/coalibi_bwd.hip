@@ -326,7 +326,9 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
     dv[dt] = f32x16{};
   }
 
-  // Work list: (query head gi, query tile qt) pairs, prefetched one ahead.
+  // Work list: (query head gi, query tile qt) pairs, prefetched one ahead.  Query tiles
+  // run from the last one down, so the key blocks of a head that run together read
+  // the same Q / dO tiles at about the same time (shared through L2).
   const int nQT = (Sq + BQ - 1) / BQ;
   const int qt0 = CAUSAL ? min((kb * kBK) / BQ, nQT) : 0;
   const int per_head = nQT - qt0;
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
   Tile qregs, doregs;
   float st_lse = 0.f, st_dsum = 0.f, st_zb = 0.f, st_cb = 0.f;  // per-row statistics for the next tile
   auto prefetch = [&](int w) {
-    const int gi = w / per_head, qt = qt0 + (w - gi * per_head);
+    const int gi = w / per_head, qt = nQT - 1 - (w - gi * per_head);
     const int bh = b * args.Hq + hkv * group + gi;
     const size_t qoff = (size_t)bh * Sq * D;
     const int q0 = qt * BQ;
@@ -352,7 +354,7 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
   if (nwork > 0) prefetch(0);
 
   for (int w = 0; w < nwork; ++w) {
-    const int gi = w / per_head, qt = qt0 + (w - gi * per_head);
+    const int gi = w / per_head, qt = nQT - 1 - (w - gi * per_head);
     const int hq = hkv * group + gi;
     const float lam = args.slopes[hq];
     const float lam2 = lam * kLog2e;
@@ -596,17 +598,19 @@ __global__ __launch_bounds__(64 * kPairWaves, 2) void coalibi_bwd_dkdv_kernel(Bw
 
   __syncthreads();  // zeroed tiles before the first DMA lands
   if (nwork > 0) {
-    issue_tile(0, qt0, 0);
-    load_stats(0, qt0);
+    issue_tile(0, nQT - 1, 0);
+    load_stats(0, nQT - 1);
     __builtin_amdgcn_s_waitcnt(0);  // the stats loads have to land before they are stored
     store_stats(0);
   }
 
-  int gi = 0, qt = qt0;  // current work item; the next one is (gn, qn)
+  // Query tiles run from the last one down: the key blocks of a head that run together
+  // then read the same Q / dO tiles at about the same time (shared through L2).
+  int gi = 0, qt = nQT - 1;  // current work item; the next one is (gn, qn)
   for (int w = 0; w < nwork; ++w) {
     const int buf = w & 1;  // statistics buffer
-    const bool wrap = qt + 1 == nQT;
-    const int gn = wrap ? gi + 1 : gi, qn = wrap ? qt0 : qt + 1;
+    const bool wrap = qt == qt0;
+    const int gn = wrap ? gi + 1 : gi, qn = wrap ? nQT - 1 : qt - 1;
     const int hq = hkv * group + gi;
     const float lam = args.slopes[hq];
     const float lam2 = lam * kLog2e;
