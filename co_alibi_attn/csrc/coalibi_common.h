@@ -75,8 +75,15 @@ __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcp
 // sigma(p) with t = p*log2(e):  1 / (1 + 2^-t)
 __device__ __forceinline__ float sigmoid_log2(float t) { return fast_rcp(1.0f + fast_exp2(-t)); }
 
-// Value held by the lane in the other half of the wavefront (l ^ 32).
-__device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32); }
+// Value held by the lane in the other half of the wavefront (l ^ 32), through
+// v_permlane32_swap (a VALU exchange, no LDS round trip).  With both operands x, the
+// instruction's first result holds x of lane l - 32 in lanes 32..63 and its second
+// result holds x of lane l + 32 in lanes 0..31.
+__device__ __forceinline__ float other_half(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
 
 // Word 3 of a gfx9-family buffer resource for raw (stride 0) dword access: 32-bit data
 // format, no swizzle.  Loads at offsets >= num_records return zero.
