@@ -52,7 +52,7 @@ _SIGNATURES = {
         [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _F, _P],
     ),
     "co_alibi_decode_workspace_bytes": (_Z, [_I, _I, _I, _I]),
-    "co_alibi_decode": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "co_alibi_decode": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _F, _P]),
     "co_alibi_last_error": (ctypes.c_char_p, []),
     "co_alibi_abi_version": (_I, []),
 }

@@ -155,29 +155,43 @@ def co_alibi_attention(q, k, v, causal=True, sm_scale=None, bias_max=8.0):
     return CoALIBIAttention.apply(q, k, v, slopes, causal, sm_scale)
 
 
-def co_alibi_decode(q, k_cache, v_cache, seq_len=None, sm_scale=None, bias_max=8.0, return_lse=False):
+def co_alibi_decode(q, k_cache, v_cache, seq_len=None, sm_scale=None, bias_max=8.0, return_lse=False,
+                    max_seq_len=None):
     """One decode step: the newest query of every head against a key / value cache.
 
     q: (B, Hq, 1, D); k_cache, v_cache: (B, Hkv, capacity, D) with the first
-    ``seq_len`` rows (default: all) of every head filled.  All of them are visible
-    to the query, so the result equals ``co_alibi_attention(q, k_cache[:, :, :seq_len],
-    v_cache[:, :, :seq_len], causal=False, sm_scale, bias_max)`` (reference
-    co_alibi_attn.py:137-148; its top-left causal mask would let an Sq = 1 query see
-    only the first key).  Inference only: no autograd record.  Returns o (B, Hq, 1, D)
-    in q.dtype, and with ``return_lse`` also the natural-log LSE (B, Hq, 1) in fp32.
+    ``seq_len`` rows of every head filled.  ``seq_len`` is an int (every sequence; default:
+    capacity) or an integer tensor of B per-sequence lengths on q's device (a serving
+    batch); then ``max_seq_len`` (default: capacity) bounds them and sizes the launch, and
+    lengths outside [0, max_seq_len] are clamped by the kernel.  All filled rows are
+    visible to the query, so the result for sequence b equals
+    ``co_alibi_attention(q[b:b+1], k_cache[b:b+1, :, :n_b], v_cache[b:b+1, :, :n_b],
+    causal=False, sm_scale, bias_max)`` (reference co_alibi_attn.py:137-148; its top-left
+    causal mask would let an Sq = 1 query see only the first key).  A sequence of length 0
+    gets O = 0 and LSE = -inf.  Inference only: no autograd record.  Returns o
+    (B, Hq, 1, D) in q.dtype, and with ``return_lse`` also the natural-log LSE (B, Hq, 1)
+    in fp32.
     """
     if q.dim() != 4 or q.shape[2] != 1:
         raise ValueError(f"q must be (B, Hq, 1, D), got {tuple(q.shape)}")
     batch_size, num_heads, _, head_dim = q.shape
     num_kv_heads, capacity = k_cache.shape[1], k_cache.shape[2]
-    if seq_len is None:
-        seq_len = capacity
     assert k_cache.shape == (batch_size, num_kv_heads, capacity, head_dim)
     assert v_cache.shape == k_cache.shape
     assert num_kv_heads >= 1 and num_heads % num_kv_heads == 0
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "Inputs must be CUDA tensors"
-    if not 1 <= seq_len <= capacity:
-        raise ValueError(f"seq_len must be in [1, {capacity}], got {seq_len}")
+    lens = None
+    if isinstance(seq_len, torch.Tensor):
+        if seq_len.shape != (batch_size,) or seq_len.dtype not in (torch.int32, torch.int64):
+            raise ValueError(f"per-sequence lengths must be an integer tensor of shape ({batch_size},)")
+        lens = seq_len.to(device=q.device, dtype=torch.int32).contiguous()
+        bound = capacity if max_seq_len is None else int(max_seq_len)
+        if not 1 <= bound <= capacity:
+            raise ValueError(f"max_seq_len must be in [1, {capacity}], got {bound}")
+    else:
+        bound = capacity if seq_len is None else int(seq_len)
+        if not 1 <= bound <= capacity:
+            raise ValueError(f"seq_len must be in [1, {capacity}], got {bound}")
     if not (q.dtype == k_cache.dtype == v_cache.dtype) or q.dtype not in _native.DTYPE_CODES:
         raise TypeError(
             f"q and the caches must share one dtype of float32/float16/bfloat16, got "
@@ -194,15 +208,15 @@ def co_alibi_decode(q, k_cache, v_cache, seq_len=None, sm_scale=None, bias_max=8
     o = torch.empty_like(q)
     lse = torch.empty((batch_size, num_heads, 1), device=q.device, dtype=torch.float32) if return_lse else None
     lib = _native.lib()
-    ws_bytes = lib.co_alibi_decode_workspace_bytes(batch_size, num_heads, seq_len, head_dim)
+    ws_bytes = lib.co_alibi_decode_workspace_bytes(batch_size, num_heads, bound, head_dim)
     workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
     with torch.cuda.device(q.device):
         _native.check(
             lib.co_alibi_decode(
                 _native.DTYPE_CODES[q.dtype], q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                slopes32.data_ptr(), o.data_ptr(), 0 if lse is None else lse.data_ptr(),
-                workspace.data_ptr(), ws_bytes, batch_size, num_heads, num_kv_heads, seq_len, capacity,
-                head_dim, float(sm_scale), _stream_handle(q.device),
+                slopes32.data_ptr(), 0 if lens is None else lens.data_ptr(), o.data_ptr(),
+                0 if lse is None else lse.data_ptr(), workspace.data_ptr(), ws_bytes, batch_size, num_heads,
+                num_kv_heads, bound, capacity, head_dim, float(sm_scale), _stream_handle(q.device),
             )
         )
     return (o, lse) if return_lse else o

@@ -273,8 +273,9 @@ size_t co_alibi_decode_workspace_bytes(int batch, int heads_q, int seq_kv, int h
 }
 
 int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v_cache, const float* slopes,
-                    void* o, float* lse, void* workspace, size_t workspace_bytes, int batch, int heads_q,
-                    int heads_kv, int seq_kv, int kv_capacity, int head_dim, float sm_scale, void* stream) {
+                    const int* seq_lens, void* o, float* lse, void* workspace, size_t workspace_bytes, int batch,
+                    int heads_q, int heads_kv, int seq_kv, int kv_capacity, int head_dim, float sm_scale,
+                    void* stream) {
   const char* fn = "co_alibi_decode";
   const Shape s{batch, heads_q, heads_kv, 1, seq_kv, head_dim};
   int rc;
@@ -288,8 +289,8 @@ int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v
                                      std::to_string(coalibi::kMaxDecodeChunks * coalibi::kDecodeChunkKeys));
   if ((rc = check_ptr(fn, "q", q, 16)) || (rc = check_ptr(fn, "k_cache", k_cache, 16)) ||
       (rc = check_ptr(fn, "v_cache", v_cache, 16)) || (rc = check_ptr(fn, "o", o, 16)) ||
-      (rc = check_ptr(fn, "slopes", slopes, 4)) || (rc = check_opt_ptr(fn, "lse", lse, 4)) ||
-      (rc = check_ptr(fn, "workspace", workspace, 256)))
+      (rc = check_ptr(fn, "slopes", slopes, 4)) || (rc = check_opt_ptr(fn, "seq_lens", seq_lens, 4)) ||
+      (rc = check_opt_ptr(fn, "lse", lse, 4)) || (rc = check_ptr(fn, "workspace", workspace, 256)))
     return rc;
   const size_t need = co_alibi_decode_workspace_bytes(batch, heads_q, seq_kv, head_dim);
   if (workspace_bytes < need)
@@ -311,6 +312,7 @@ int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v
   a.psum = reinterpret_cast<float*>(ws + stat_bytes);
   a.psig = reinterpret_cast<float*>(ws + 2 * stat_bytes);
   a.pout = reinterpret_cast<float*>(ws + 3 * stat_bytes);
+  a.seq_lens = seq_lens;
   a.B = batch;
   a.Hq = heads_q;
   a.Hkv = heads_kv;

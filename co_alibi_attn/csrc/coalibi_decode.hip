@@ -94,12 +94,24 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void coalibi_decode_split_kernel
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane & 31, hh = lane >> 5;
   const int split = blockIdx.x, bhk = blockIdx.y;
-  const int G = a.G, L = a.L, nS = a.nSplits;
+  const int G = a.G, nS = a.nSplits;
   const int b = bhk / a.Hkv, hkv = bhk - b * a.Hkv;
+  // This sequence's cache length (per-sequence lengths clamped to [0, L]).
+  const int L = a.seq_lens == nullptr ? a.L : min(max(a.seq_lens[b], 0), a.L);
   const int hq0 = hkv * G;  // first query head of the group
   const size_t bh0 = (size_t)b * a.Hq + hq0;
   const int c_first = split * a.cps;
-  const int c_last = min(c_first + a.cps, a.nChunks) - 1;
+  const int c_last = min(c_first + a.cps, (L + kDecodeChunkKeys - 1) / kDecodeChunkKeys) - 1;
+  if (c_last < c_first) {  // the split lies past this sequence's length: an empty partial
+    for (int i = tid; i < G * D; i += kDecWaves * 64) a.pout[((bh0 + i / D) * nS + split) * D + i % D] = 0.f;
+    if (tid < G) {
+      const size_t pi = (bh0 + tid) * nS + split;
+      a.pmax[pi] = kNegInf;
+      a.psum[pi] = 0.f;
+      a.psig[pi] = 0.f;
+    }
+    return;
+  }
   const T* const kbase = static_cast<const T*>(a.k) + (size_t)bhk * a.cap * D;
   const T* const vbase = static_cast<const T*>(a.v) + (size_t)bhk * a.cap * D;
   T* const sVw = sV + wave * C::WAVE_ELEMS;
@@ -286,7 +298,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void coalibi_decode_split_kernel
       l += f * sSum[w][h];
     }
     const size_t pi = (bh0 + h) * nS + split;
-    a.pmax[pi] = m;  // finite: the split's first key is below L
+    a.pmax[pi] = m;  // finite: the split's first key is below this sequence's length
     a.psum[pi] = l;
     a.psig[pi] = carry;
   }
@@ -380,9 +392,12 @@ __global__ __launch_bounds__(kDecMergeThreads) void coalibi_decode_merge_kernel(
 #pragma unroll
   for (int w = 0; w < NW; ++w) m = fmaxf(m, sRed[w]);
   __syncthreads();
+  // Empty splits (past a sequence's length) have maximum -inf and weight 0; a sequence
+  // of length 0 has no split with a key: O = 0 and LSE = -inf.
+  const float mref = m == kNegInf ? 0.f : m;
   float l = 0.f;
   for (int c = tid; c < nS; c += kDecMergeThreads) {
-    const float w = fast_exp2(sW[c] - m);
+    const float w = fast_exp2(sW[c] - mref);
     sW[c] = w;
     l += w * psum[c];
   }
@@ -411,8 +426,8 @@ __global__ __launch_bounds__(kDecMergeThreads) void coalibi_decode_merge_kernel(
     float s = 0.f;
 #pragma unroll
     for (int p = 0; p < PARTS; ++p) s += sAcc[p][tid];
-    static_cast<T*>(a.o)[bh * D + tid] = static_cast<T>(s / l);
-    if (tid == 0 && a.lse != nullptr) a.lse[bh] = (m + log2f(l)) * kLn2;
+    static_cast<T*>(a.o)[bh * D + tid] = static_cast<T>(l > 0.f ? s / l : 0.f);
+    if (tid == 0 && a.lse != nullptr) a.lse[bh] = l > 0.f ? (m + log2f(l)) * kLn2 : kNegInf;
   }
 }
 

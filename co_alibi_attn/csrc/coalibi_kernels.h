@@ -46,9 +46,10 @@ struct BwdArgs {
 };
 
 // Decode: q/o (B, Hq, D); the caches k/v are (B, Hkv, cap, D) with the first L rows
-// of every head valid.  The keys form nChunks chunks of kDecodeChunkKeys; split s of a
-// head covers chunks [s*cps, (s+1)*cps).  Split-K partials per (b*Hq + h, split):
-// pmax / psum / psig (B*Hq, nSplits) and pout (B*Hq, nSplits, D), fp32.
+// of every head valid (or the first seq_lens[b] rows of sequence b, at most L).  The
+// keys form nChunks chunks of kDecodeChunkKeys; split s of a head covers chunks
+// [s*cps, (s+1)*cps).  Split-K partials per (b*Hq + h, split): pmax / psum / psig
+// (B*Hq, nSplits) and pout (B*Hq, nSplits, D), fp32.
 constexpr int kDecodeChunkKeys = 256;
 constexpr int kMaxDecodeGroup = 32;     // query heads per kv head (MFMA tile columns)
 constexpr int kMaxDecodeChunks = 8192;  // chunk weights held in LDS by the merge
@@ -64,6 +65,7 @@ struct DecodeArgs {
   float* psum;
   float* psig;
   float* pout;
+  const int* seq_lens;  // (B,) per-sequence cache lengths, or NULL (all L)
   int B, Hq, Hkv, G, L, cap, nChunks, cps, nSplits;
   float sc2;
 };

@@ -144,7 +144,7 @@ class DecodeSet:
         self.stream = torch.cuda.current_stream(dev)
         code = _native.DTYPE_CODES[w.dtype]
         p = lambda t: t.data_ptr()  # noqa: E731
-        args = (code, p(self.q), p(self.k), p(self.v), p(self.lam), p(self.o), p(self.lse), p(self.ws),
+        args = (code, p(self.q), p(self.k), p(self.v), p(self.lam), 0, p(self.o), p(self.lse), p(self.ws),
                 self.ws_bytes, B, Hq, Hkv, L, L, D, 1.0 / math.sqrt(D), self.stream.cuda_stream)
 
         def step():

@@ -11,6 +11,9 @@
  *                 in co_alibi_attn/co_alibi_attn.py:101-123 together with the
  *                 dK/dV partial buffers and their reduction (:83-99, :132-133).
  *
+ * and a decode step the reference does not have, co_alibi_decode: its forward
+ * with Sq = 1 over a key / value cache, as one split-K pass over the cache.
+ *
  * Tensor layout: contiguous row-major, q / o / dout / dq are (B, Hq, Sq, D),
  * k / v / dk / dv are (B, Hkv, Skv, D); query head h attends key/value head
  * h / (Hq / Hkv) (the head mapping of co_alibi_attn.py:143-146, done in-kernel
@@ -91,19 +94,21 @@ int co_alibi_bwd_dkdv(int dtype, const void* dout, const void* q, const void* k,
 size_t co_alibi_decode_workspace_bytes(int batch, int heads_q, int seq_kv, int head_dim);
 
 /* Decode: one new query per (batch, query head) against a key / value cache.
- * q and o are (B, Hq, D); k_cache and v_cache are (B, Hkv, kv_capacity, D) with the
- * first seq_kv rows of every head valid, all of them visible to the query (the
- * newest position).  lse (B*Hq fp32, natural log) may be NULL.  The reference has
- * no decode entry point: this is its forward, co_alibi_attention(q, k, v,
- * causal=False) (co_alibi_attn/co_alibi_attn.py:137-148), with Sq = 1 and the
- * caches cut to seq_kv rows; its top-left causal mask (co_alibi_fwd_kernel.py:80-90)
+ * q and o are (B, Hq, D); k_cache and v_cache are (B, Hkv, kv_capacity, D).  Sequence
+ * b has its first len_b rows of every head filled, all of them visible to the query
+ * (the newest position): len_b = seq_lens[b] when seq_lens (B int32 on the device) is
+ * given, clamped to [0, seq_kv] in the kernel, else seq_kv.  A sequence of length 0
+ * gets O = 0 and LSE = -inf.  lse (B*Hq fp32, natural log) may be NULL.  The
+ * reference has no decode entry point: this is its forward, co_alibi_attention(q, k,
+ * v, causal=False) (co_alibi_attn/co_alibi_attn.py:137-148), with Sq = 1 and the
+ * caches cut to len_b rows; its top-left causal mask (co_alibi_fwd_kernel.py:80-90)
  * would show an Sq = 1 query only the first key.  At most 32 query heads per kv
- * head, seq_kv <= 2^21; workspace holds co_alibi_decode_workspace_bytes(...) bytes
- * (256-byte aligned). */
+ * head, seq_kv <= 2^21 (it sizes the grid and the workspace); workspace holds
+ * co_alibi_decode_workspace_bytes(...) bytes (256-byte aligned). */
 int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v_cache,
-                    const float* slopes, void* o, float* lse, void* workspace,
-                    size_t workspace_bytes, int batch, int heads_q, int heads_kv, int seq_kv,
-                    int kv_capacity, int head_dim, float sm_scale, void* stream);
+                    const float* slopes, const int* seq_lens, void* o, float* lse,
+                    void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv,
+                    int seq_kv, int kv_capacity, int head_dim, float sm_scale, void* stream);
 
 /* Message describing the last failed call on this thread ("" if none). */
 const char* co_alibi_last_error(void);

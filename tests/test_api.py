@@ -120,16 +120,17 @@ def test_decode_sizes():
 
 
 def _decode(lib, **over):
-    args = dict(dtype=1, q=256, k=256, v=256, slopes=256, o=256, lse=None, ws=256, ws_bytes=1 << 20, B=1, Hq=8,
+    args = dict(dtype=1, q=256, k=256, v=256, slopes=256, lens=None, o=256, lse=None, ws=256, ws_bytes=1 << 20, B=1, Hq=8,
                 Hkv=2, L=300, cap=512, D=128, scale=0.125)
     args.update(over)
-    return lib.co_alibi_decode(args["dtype"], args["q"], args["k"], args["v"], args["slopes"], args["o"],
-                               args["lse"], args["ws"], args["ws_bytes"], args["B"], args["Hq"], args["Hkv"],
-                               args["L"], args["cap"], args["D"], args["scale"], None)
+    return lib.co_alibi_decode(args["dtype"], args["q"], args["k"], args["v"], args["slopes"], args["lens"],
+                               args["o"], args["lse"], args["ws"], args["ws_bytes"], args["B"], args["Hq"],
+                               args["Hkv"], args["L"], args["cap"], args["D"], args["scale"], None)
 
 
 @pytest.mark.parametrize("over,code,msg", [
     (dict(k=None), 1, "k_cache is NULL"),
+    (dict(lens=2), 1, "seq_lens is not 4-byte aligned"),
     (dict(v=8), 1, "v_cache is not 16-byte aligned"),
     (dict(ws=16), 1, "workspace is not 256-byte aligned"),
     (dict(ws_bytes=1000), 1, "workspace of 1000 bytes"),

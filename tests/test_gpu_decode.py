@@ -128,3 +128,36 @@ def test_decode_is_deterministic_and_lse_optional():
     torch.cuda.synchronize()
     assert torch.equal(a, b)
     assert lse.shape == (B, Hq, 1) and lse.dtype == torch.float32
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_decode_per_sequence_lengths(dtype):
+    """A serving batch: each sequence against its own filled prefix of the cache (lengths 1 .. capacity, and 0)."""
+    B, Hq, Hkv, cap, D = 5, 16, 4, 1500, 128
+    lens = [700, 1, 1500, 0, 257]
+    q, k, v = cache_inputs(B, Hq, Hkv, cap, cap, D, dtype, seed=21)
+    for b, n in enumerate(lens):  # rows past each sequence's length hold garbage that must not leak in
+        k[b, :, n:] = 100.0
+        v[b, :, n:] = -1000.0
+    seq = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    o, lse = co_alibi_decode(q.to(DEV), k.to(DEV), v.to(DEV), seq_len=seq, return_lse=True)
+    torch.cuda.synchronize()
+    for b, n in enumerate(lens):
+        if n == 0:
+            assert torch.equal(o[b].float().cpu(), torch.zeros(Hq, 1, D)), "empty sequence: O must be 0"
+            assert torch.isneginf(lse[b]).all(), "empty sequence: LSE must be -inf"
+            continue
+        ro, rlse = oracle_decode(q[b:b + 1], k[b:b + 1], v[b:b + 1], n)
+        check(f"o[{b}] (len {n})", o[b:b + 1], ro, TOL[dtype])
+        check(f"lse[{b}] (len {n})", lse[b:b + 1], rlse, TOL[dtype])
+
+
+def test_decode_lengths_are_clamped_to_the_bound():
+    """Per-sequence lengths past max_seq_len count as max_seq_len (the kernel clamps device data)."""
+    B, Hq, Hkv, cap, D = 2, 8, 2, 2048, 64
+    q, k, v = (t.to(DEV) for t in cache_inputs(B, Hq, Hkv, cap, cap, D, torch.float16, seed=4))
+    seq = torch.tensor([5000, 1000], dtype=torch.int32, device=DEV)
+    got = co_alibi_decode(q, k, v, seq_len=seq, max_seq_len=1000)
+    want = co_alibi_decode(q, k, v, seq_len=1000)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
