@@ -14,7 +14,7 @@ import torch  # noqa: F401  (must be imported before the HIP library is loaded)
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libco_alibi.so")
 
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
-SUPPORTED_HEAD_DIMS = (32, 64, 128)
+SUPPORTED_HEAD_DIMS = (32, 64, 128, 256)
 
 # Symbols declared in include/co_alibi.h.
 EXPORTS = (

@@ -44,6 +44,13 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _check_head_dim(head_dim: int, dtype: torch.dtype) -> None:
+    if head_dim not in _native.SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {_native.SUPPORTED_HEAD_DIMS}, got {head_dim}")
+    if head_dim == 256 and dtype == torch.float32:
+        raise ValueError("head_dim 256 needs float16 or bfloat16 inputs")
+
+
 def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -64,8 +71,7 @@ def _forward(q, k, v, slopes, causal, sm_scale, with_stats: bool):
     assert slopes.shape == (num_heads,), f"Slopes shape {slopes.shape} doesn't match num_heads {num_heads}"
     if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _native.DTYPE_CODES:
         raise TypeError(f"q, k, v must share one dtype of float32/float16/bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
-    if head_dim not in _native.SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"head_dim must be one of {_native.SUPPORTED_HEAD_DIMS}, got {head_dim}")
+    _check_head_dim(head_dim, q.dtype)
 
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     slopes32 = slopes.detach().to(device=q.device, dtype=torch.float32).contiguous()
@@ -197,8 +203,7 @@ def co_alibi_decode(q, k_cache, v_cache, seq_len=None, sm_scale=None, bias_max=8
             f"q and the caches must share one dtype of float32/float16/bfloat16, got "
             f"{q.dtype}, {k_cache.dtype}, {v_cache.dtype}"
         )
-    if head_dim not in _native.SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"head_dim must be one of {_native.SUPPORTED_HEAD_DIMS}, got {head_dim}")
+    _check_head_dim(head_dim, q.dtype)
     if sm_scale is None:
         sm_scale = 1.0 / (head_dim ** 0.5)
 

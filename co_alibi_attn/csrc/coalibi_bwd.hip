@@ -131,7 +131,7 @@ __device__ __forceinline__ void dp_tile(const f32x16& sacc, f32x16& dacc, float 
 // Pass 1: dQ, D, cb.  Per wavefront 32 query rows; register r of lane (col, hh)
 // <-> key k0 + hh*16 + r.
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_bwd_dq_kernel(BwdArgs args) {
+__global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coalibi_bwd_dq_kernel(BwdArgs args) {
   using C = BwdCfg<T, D>;
   using M = Mfma<T>;
   using vec8 = typename M::vec8;
@@ -489,7 +489,7 @@ constexpr int kPairWaves = 4;   // wavefronts per work-group: 2 key groups x 2 q
 // Two work-groups per CU: 77 KB of LDS and at most 256 VGPRs each.
 
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(64 * kPairWaves, 2) void coalibi_bwd_dkdv_kernel(BwdArgs args) {
+__global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_dkdv_kernel(BwdArgs args) {
   static_assert(sizeof(T) == 2, "the wavefront-pair pass 2 is the 16-bit path");
   using C = BwdCfg<T, D>;
   using M = Mfma<T>;
@@ -738,9 +738,11 @@ hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream) {
 COALIBI_INST_BWD(_Float16, 32)
 COALIBI_INST_BWD(_Float16, 64)
 COALIBI_INST_BWD(_Float16, 128)
+COALIBI_INST_BWD(_Float16, 256)
 COALIBI_INST_BWD(__bf16, 32)
 COALIBI_INST_BWD(__bf16, 64)
 COALIBI_INST_BWD(__bf16, 128)
+COALIBI_INST_BWD(__bf16, 256)
 COALIBI_INST_BWD(float, 32)
 COALIBI_INST_BWD(float, 64)
 COALIBI_INST_BWD(float, 128)

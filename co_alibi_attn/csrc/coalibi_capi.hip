@@ -37,9 +37,13 @@ int check_shape(const char* fn, int dtype, const Shape& s) {
     return fail(CO_ALIBI_EINVAL, std::string(fn) + ": batch, heads and sequence lengths must be >= 1");
   if (s.Hq % s.Hkv != 0)
     return fail(CO_ALIBI_EINVAL, std::string(fn) + ": heads_q must be a multiple of heads_kv");
-  if (s.D != 32 && s.D != 64 && s.D != 128)
+  if (s.D != 32 && s.D != 64 && s.D != 128 && s.D != 256)
     return fail(CO_ALIBI_EUNSUPPORTED,
-                std::string(fn) + ": head_dim must be 32, 64 or 128, got " + std::to_string(s.D));
+                std::string(fn) + ": head_dim must be 32, 64, 128 or 256, got " + std::to_string(s.D));
+  // fp32 tiles at D = 256 exceed the register file in backward pass 2 (fragments and
+  // accumulators of 32 keys x 256 dims in fp32).
+  if (s.D == 256 && dtype == CO_ALIBI_F32)
+    return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": head_dim 256 needs fp16 or bf16");
   // Sequence indices are 32-bit in the kernels; grids must fit a 31-bit launch.
   const double wg = std::ceil(s.Sq / 128.0) * s.B * s.Hq;
   if (s.Sq > (1 << 30) || s.Skv > (1 << 30) || wg > 2147483647.0)
@@ -71,6 +75,9 @@ hipError_t fwd_dispatch_d(const coalibi::FwdArgs& a, int D, bool causal, hipStre
   switch (D) {
     case 32: return fwd_dispatch_causal<T, 32>(a, causal, st);
     case 64: return fwd_dispatch_causal<T, 64>(a, causal, st);
+    case 256:
+      if constexpr (sizeof(T) == 2) return fwd_dispatch_causal<T, 256>(a, causal, st);
+      return hipErrorInvalidValue;
     default: return fwd_dispatch_causal<T, 128>(a, causal, st);
   }
 }
@@ -85,6 +92,9 @@ hipError_t bwd_dispatch_d(const coalibi::BwdArgs& a, int D, bool causal, int sta
   switch (D) {
     case 32: return bwd_dispatch_causal<T, 32>(a, causal, stages, st);
     case 64: return bwd_dispatch_causal<T, 64>(a, causal, stages, st);
+    case 256:
+      if constexpr (sizeof(T) == 2) return bwd_dispatch_causal<T, 256>(a, causal, stages, st);
+      return hipErrorInvalidValue;
     default: return bwd_dispatch_causal<T, 128>(a, causal, stages, st);
   }
 }
@@ -241,6 +251,9 @@ hipError_t decode_dispatch_d(const coalibi::DecodeArgs& a, int D, hipStream_t st
   switch (D) {
     case 32: return coalibi::launch_decode<T, 32>(a, st);
     case 64: return coalibi::launch_decode<T, 64>(a, st);
+    case 256:
+      if constexpr (sizeof(T) == 2) return coalibi::launch_decode<T, 256>(a, st);
+      return hipErrorInvalidValue;
     default: return coalibi::launch_decode<T, 128>(a, st);
   }
 }

@@ -79,11 +79,14 @@ __device__ __forceinline__ typename Mfma<T>::vec8 ld_kmajor_dec(const T* tile, i
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 template <typename T, int D>
-__global__ __launch_bounds__(kDecWaves * 64, 2) void coalibi_decode_split_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kDecWaves * 64, D > 128 ? 1 : 2) void coalibi_decode_split_kernel(DecodeArgs a) {
   using M = Mfma<T>;
   using V8 = typename M::vec8;
   using C = DecCfg<T, D>;
   constexpr int kKLoads = 2 * C::KS * (sizeof(T) == 4 ? 2 : 1);  // buffer loads per K fragment set
+  // The next chunk's K loads during this chunk's math; at D = 256 its registers do not
+  // fit beside the chunk state and it is loaded after P V instead.
+  constexpr bool kPrefetch = D <= 128;
   __shared__ __align__(16) T sV[kDecWaves * C::WAVE_ELEMS];
   __shared__ float sSig[2][kDecWaves][kMaxDecodeGroup];  // per-wavefront sigma totals (by chunk parity)
   __shared__ float sMax[kDecWaves][kMaxDecodeGroup];
@@ -182,7 +185,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void coalibi_decode_split_kernel
     }
     // The K fragments are consumed: the next chunk's load into them while this one finishes
     // (tile 0 now, tile 1 before P V, which keeps 32 fewer registers live meanwhile).
-    if (more) load_k_tile(kf[0], c - 1, 0);
+    if (kPrefetch && more) load_k_tile(kf[0], c - 1, 0);
 
     // Scores and sigma.  Key order over the lanes: tile 0 half 0, tile 0 half 1, tile 1
     // half 0, tile 1 half 1.  Keys past L get t = -inf: their sigma is 0 and their a and
@@ -262,7 +265,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void coalibi_decode_split_kernel
     }
 
     // V of this chunk has landed once at most the next chunk's K loads are outstanding.
-    if (more) {
+    if (kPrefetch && more) {
       load_k_tile(kf[1], c - 1, 1);
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKLoads));
     } else {
@@ -276,7 +279,13 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void coalibi_decode_split_kernel
         for (int s = 0; s < 2; ++s)
           oacc[j] = M::k16(pa[i][s], ld_kmajor_dec<T>(sVw, C::LD, 32 * i + 8 * s, 16, 32 * j, lane), oacc[j]);
 
-    if (more) issue_v(row0 - kDecodeChunkKeys);
+    if (more) {
+      if constexpr (!kPrefetch) {
+        load_k_tile(kf[0], c - 1, 0);
+        load_k_tile(kf[1], c - 1, 1);
+      }
+      issue_v(row0 - kDecodeChunkKeys);
+    }
   }
 
   // Combine the wavefronts (their maxima share one z frame: the split's own keys).
@@ -447,9 +456,11 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
 COALIBI_INST_DEC(_Float16, 32)
 COALIBI_INST_DEC(_Float16, 64)
 COALIBI_INST_DEC(_Float16, 128)
+COALIBI_INST_DEC(_Float16, 256)
 COALIBI_INST_DEC(__bf16, 32)
 COALIBI_INST_DEC(__bf16, 64)
 COALIBI_INST_DEC(__bf16, 128)
+COALIBI_INST_DEC(__bf16, 256)
 COALIBI_INST_DEC(float, 32)
 COALIBI_INST_DEC(float, 64)
 COALIBI_INST_DEC(float, 128)

@@ -162,7 +162,7 @@ __device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __re
 }
 
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kernel(FwdArgs args) {
+__global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coalibi_fwd_kernel(FwdArgs args) {
   using C = FwdCfg<T, D>;
   using M = Mfma<T>;
   using vec8 = typename M::vec8;
@@ -227,12 +227,22 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
     else
       vt_regs.store_cols(sV, C::LDV, tid);
     __syncthreads();
-    if (kt > 0) {
+    // The next tile's K / V go into registers during this tile's math; at D = 256 those
+    // registers do not fit beside the tile state, and the loads are issued after it.
+    constexpr bool kPrefetchKV = D <= 128;
+    if (kPrefetchKV && kt > 0) {
       kt_regs.load(Kp, (kt - 1) * kFwdBN, Skv, tid);
       vt_regs.load(Vp, (kt - 1) * kFwdBN, Skv, tid);
     }
     const int k0 = kt * kFwdBN;
-    if (CAUSAL && k0 > wrow0 + 31) continue;  // every key of the tile is above this wavefront's rows
+    const bool skip = CAUSAL && k0 > wrow0 + 31;  // every key of the tile is above this wavefront's rows
+    if (skip) {
+      if (!kPrefetchKV && kt > 0) {
+        kt_regs.load(Kp, (kt - 1) * kFwdBN, Skv, tid);
+        vt_regs.load(Vp, (kt - 1) * kFwdBN, Skv, tid);
+      }
+      continue;
+    }
     const bool masked = (CAUSAL && k0 + kFwdBN - 1 > wrow0) || (k0 + kFwdBN > Skv);
     float zst0, zst1;
     if (masked)
@@ -244,6 +254,10 @@ __global__ __launch_bounds__(256, sizeof(T) == 4 ? 1 : 2) void coalibi_fwd_kerne
     if (write_zb && hh == 0 && row_ok) {
       zb_row[(size_t)(2 * kt) * Sq] = zst0;
       if (k0 + 32 < Skv) zb_row[(size_t)(2 * kt + 1) * Sq] = zst1;
+    }
+    if (!kPrefetchKV && kt > 0) {
+      kt_regs.load(Kp, (kt - 1) * kFwdBN, Skv, tid);
+      vt_regs.load(Vp, (kt - 1) * kFwdBN, Skv, tid);
     }
   }
 
@@ -286,9 +300,11 @@ hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
 COALIBI_INST_FWD(_Float16, 32)
 COALIBI_INST_FWD(_Float16, 64)
 COALIBI_INST_FWD(_Float16, 128)
+COALIBI_INST_FWD(_Float16, 256)
 COALIBI_INST_FWD(__bf16, 32)
 COALIBI_INST_FWD(__bf16, 64)
 COALIBI_INST_FWD(__bf16, 128)
+COALIBI_INST_FWD(__bf16, 256)
 COALIBI_INST_FWD(float, 32)
 COALIBI_INST_FWD(float, 64)
 COALIBI_INST_FWD(float, 128)

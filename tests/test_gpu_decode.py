@@ -54,6 +54,22 @@ CASES = [
     (2, 16, 16, 257, 300, 128),     # no grouping, one key past a chunk
     (1, 32, 8, 4113, 4113, 128),    # Llama-style 4:1 grouping, ragged tail
 ]
+# Head dim 256 (fp16 / bf16 only).
+CASES_D256 = [
+    (2, 8, 2, 1300, 1536, 256),
+]
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16), ids=("float16", "bfloat16"))
+@pytest.mark.parametrize("case", CASES_D256, ids=lambda c: "B{}_Hq{}_Hkv{}_L{}_cap{}_D{}".format(*c))
+def test_decode_head_dim_256(case, dtype):
+    B, Hq, Hkv, L, cap, D = case
+    q, k, v = cache_inputs(B, Hq, Hkv, L, cap, D, dtype, seed=L)
+    o, lse = co_alibi_decode(q.to(DEV), k.to(DEV), v.to(DEV), seq_len=L, return_lse=True)
+    torch.cuda.synchronize()
+    ro, rlse = oracle_decode(q, k, v, L)
+    check("o", o, ro, TOL[dtype])
+    check("lse", lse, rlse, TOL[dtype])
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])

@@ -206,9 +206,30 @@ def test_sm_scale_and_bias_max_arguments():
     assert_parity(got, (o, dq, dk, dv), 1e-4, "sm_scale=0.3 bias_max=4 H=3")
 
 
+# Head dim 256: fp16 / bf16 only (fp32 pass 2 would not fit the register file).
+CASES_D256 = [
+    (1, 2, 2, 200, 200, 256, True),     # two query blocks, partial last key tile
+    (1, 4, 2, 70, 150, 256, False),     # non-causal, rectangular, grouped
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("case", CASES_D256, ids=lambda c: "B{}H{}/{}S{}x{}D{}{}".format(*c[:6], "c" if c[6] else "n"))
+def test_head_dim_256(case, dtype):
+    B, Hq, Hkv, Sq, Skv, D, causal = case
+    print(f"case {case} {dtype}", flush=True)
+    q, k, v, do = rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=2)
+    got = hip_fwd_bwd(q, k, v, do, causal=causal)
+    o, lse, dq, dk, dv = oracle_fwd_bwd(q, k, v, do, causal=causal)
+    assert_parity(got, (o, dq, dk, dv), TOL[dtype], f"{case}")
+
+
 def test_unsupported_inputs_raise():
     q = torch.randn(1, 2, 8, 96, device=DEV, dtype=torch.float16)
     with pytest.raises(ValueError, match="head_dim"):
+        co_alibi_attention(q, q, q)
+    q = torch.randn(1, 2, 8, 256, device=DEV, dtype=torch.float32)
+    with pytest.raises(ValueError, match="256"):
         co_alibi_attention(q, q, q)
     q = torch.randn(1, 2, 8, 64, device=DEV, dtype=torch.float64)
     with pytest.raises(TypeError):
