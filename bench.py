@@ -12,6 +12,9 @@ Also measured in the same run:
     in ``roofline`` against the dense fp16 MFMA peak, with the HBM traffic per
     launch that the rocprofv3 FETCH_SIZE/WRITE_SIZE passes recorded in
     profiles/traffic_<workload>.md (null when that file is absent);
+  * the box's sustained MFMA ceiling (``mfma_ceiling``): a probe kernel issuing only
+    fp16 MFMAs on every CU for ~10 ms, its rate and clock (sustained MFMA load lowers
+    the clock below the 2.4 GHz of the published peak), and the fractions against it;
   * the CPU baseline: the repository's CPU restatement of model.py (oracle,
     fp32) on a time-bounded sample of the same workload;
   * decode steps (``co_alibi_decode``: one query per head against a key/value
@@ -283,6 +286,14 @@ def main():
     traffic = read_traffic(os.path.join(ROOT, "profiles", f"traffic_{w.name}.md")).get(dominant)
     print(f"[bench] per-kernel: {json.dumps(per_kernel)}", file=sys.stderr, flush=True)
 
+    # The published peak assumes 2.4 GHz.  The box's own MFMA ceiling: a probe kernel that
+    # issues only fp16 MFMAs on every CU for ~10 ms (its clock is the shader-clock /
+    # real-time counter ratio; sustained MFMA load lowers the clock).
+    from co_alibi_attn.profiling import mfma_probe
+
+    probe_tflops, clock_ghz = mfma_probe(dev)
+    print(f"[bench] MFMA probe: {probe_tflops:.0f} TFLOP/s, clock {clock_ghz:.3f} GHz", file=sys.stderr, flush=True)
+
     sdpa_ms = None
     if args.sdpa and w.heads_q == w.heads_kv:
         # Plain causal attention at the same shape and dtype (torch SDPA on ROCm), fwd + bwd:
@@ -333,6 +344,10 @@ def main():
         "ref_convention_tflops": {"fwd": round(2 * fwd_flops / (fwd_ms * 1e-3) / 1e12, 2),
                                   "bwd": round(4 * fwd_flops / (bwd_ms * 1e-3) / 1e12, 2)},
         "kernels": per_kernel,
+        "mfma_ceiling": {"probe_fp16_tflops": round(probe_tflops, 1), "clock_ghz": round(clock_ghz, 3),
+                         "fwd_frac": round(fwd_flops / (fwd_ms * 1e-3) / 1e12 / probe_tflops, 4),
+                         "bwd_frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / probe_tflops, 4),
+                         "dominant_kernel_frac": round(achieved / probe_tflops, 4)},
         "sdpa_ms_per_step": None if sdpa_ms is None else round(sdpa_ms, 4),
         "coalibi_over_sdpa": None if sdpa_ms is None else round(ms_step / sdpa_ms, 3),
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",

@@ -18,7 +18,7 @@ OBJ_DIR = os.path.join(PKG_DIR, "_build")
 LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libco_alibi.so")
 ARCH = "gfx950"
-SOURCES = ("coalibi_fwd.hip", "coalibi_bwd.hip", "coalibi_decode.hip", "coalibi_capi.hip")
+SOURCES = ("coalibi_fwd.hip", "coalibi_bwd.hip", "coalibi_decode.hip", "coalibi_probe.hip", "coalibi_capi.hip")
 
 # Packed fp32 VALU forms are disabled for all device code (the compiler would
 # otherwise form v_pk_{add,mul,fma}_f32 from scalar float code).

@@ -26,6 +26,7 @@ EXPORTS = (
     "co_alibi_bwd_dkdv",
     "co_alibi_decode_workspace_bytes",
     "co_alibi_decode",
+    "co_alibi_probe_mfma",
     "co_alibi_last_error",
     "co_alibi_abi_version",
 )
@@ -53,6 +54,7 @@ _SIGNATURES = {
     ),
     "co_alibi_decode_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "co_alibi_decode": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "co_alibi_probe_mfma": (_I, [_P, _P, _I, _I, _P]),
     "co_alibi_last_error": (ctypes.c_char_p, []),
     "co_alibi_abi_version": (_I, []),
 }

@@ -168,6 +168,39 @@ class DecodeSet:
         return e0.elapsed_time(e1) / reps
 
 
+def mfma_probe(device="cuda:0", iters: int = 20000, per_cu: int = 2):
+    """Sustained MFMA rate and shader clock under MFMA load on every CU.
+
+    Returns (tflops, clock_ghz): fp16 MFMA TFLOP/s from the probe's wall time (HIP events),
+    and the clock from the shader-clock / 100 MHz real-time counter ratio of its loops.
+    """
+    import torch
+
+    from co_alibi_attn import _native
+
+    lib = _native.lib()
+    dev = torch.device(device)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    blocks = cus * per_cu
+    ticks = torch.zeros(2 * blocks, dtype=torch.int64, device=dev)
+    sink = torch.empty(256 * blocks, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    run = lambda: _native.check(lib.co_alibi_probe_mfma(ticks.data_ptr(), sink.data_ptr(), blocks, iters,  # noqa: E731
+                                                         stream.cuda_stream))
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    run()
+    e1.record(stream)
+    e1.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3
+    flops = blocks * 4 * iters * 4 * 2.0 * 32 * 32 * 16  # waves x rounds x MFMAs x flops
+    t = ticks.view(blocks, 2).double().cpu()
+    clock_ghz = float((t[:, 0] / t[:, 1]).median()) * 0.1  # shader ticks per 10 ns tick
+    return flops / sec / 1e12, clock_ghz
+
+
 def calibration_copy(device="cuda:0", nbytes: int = CALIBRATION_BYTES) -> None:
     """A device-to-device copy of ``nbytes``: it reads and writes exactly ``nbytes`` of HBM."""
     import torch

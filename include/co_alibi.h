@@ -110,6 +110,13 @@ int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v
                     void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv,
                     int seq_kv, int kv_capacity, int head_dim, float sm_scale, void* stream);
 
+/* Measurement helper with no counterpart in the reference: `blocks` work-groups of 256
+ * threads each issue `iters` rounds of four independent fp16 32x32x16 MFMAs per
+ * wavefront.  ticks (2*blocks uint64) receives, per work-group, the shader-clock and the
+ * 100 MHz real-time counter deltas around the loop; sink (256*blocks fp32) receives a
+ * checksum.  The benchmark derives the sustained clock and MFMA rate from it. */
+int co_alibi_probe_mfma(void* ticks, void* sink, int blocks, int iters, void* stream);
+
 /* Message describing the last failed call on this thread ("" if none). */
 const char* co_alibi_last_error(void);
 
