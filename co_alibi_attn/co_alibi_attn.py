@@ -5,15 +5,16 @@ Same public surface as the reference module co_alibi_attn/co_alibi_attn.py:
 (reference :137-148), the autograd function ``CoALIBIAttention`` (:24-135) and
 the slope helper ``_get_coalibi_slopes`` (:11-22), plus ``co_alibi_decode``, a
 split-K decode step over a key / value cache that the reference lacks.  The work runs in the
-hand-written gfx950 kernels of ``libco_alibi.so`` (C ABI in include/co_alibi.h);
-grouped-query attention is handled inside the kernels instead of by
-``repeat_interleave``.
+hand-written gfx950 kernels of ``libco_alibi.so`` (C ABI in include/co_alibi.h), reached
+through the torch operators ``co_alibi::fwd``, ``co_alibi::bwd`` and ``co_alibi::decode``
+(co_alibi_attn/ops.py); grouped-query attention is handled inside the kernels instead of
+by ``repeat_interleave``.
 """
 from __future__ import annotations
 
 import torch
 
-from . import _native
+from . import _native, ops
 
 __all__ = ["co_alibi_attention", "co_alibi_decode", "CoALIBIAttention", "_get_coalibi_slopes"]
 
@@ -36,14 +37,6 @@ def _get_coalibi_slopes(n_heads: int, bias_max: float = 8.0) -> torch.Tensor:
     return slopes.abs()
 
 
-def _aligned(t: torch.Tensor) -> torch.Tensor:
-    """Contiguous tensor whose data pointer is 16-byte aligned (what the kernels load)."""
-    t = t.contiguous()
-    if t.data_ptr() % 16 != 0:
-        t = t.clone()
-    return t
-
-
 def _check_head_dim(head_dim: int, dtype: torch.dtype) -> None:
     if head_dim not in _native.SUPPORTED_HEAD_DIMS:
         raise ValueError(f"head_dim must be one of {_native.SUPPORTED_HEAD_DIMS}, got {head_dim}")
@@ -51,19 +44,11 @@ def _check_head_dim(head_dim: int, dtype: torch.dtype) -> None:
         raise ValueError("head_dim 256 needs float16 or bfloat16 inputs")
 
 
-def _stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
-
-
-def _forward(q, k, v, slopes, causal, sm_scale, with_stats: bool):
-    """Checks (as the reference's co_alibi_attn.py:30-33) and the native forward.
-
-    Returns (o, lse, zb); with ``with_stats=False`` (inference) lse and zb are
-    None and the kernel writes neither.
-    """
-    batch_size, num_heads, seq_len_q, head_dim = q.shape
+def _check_inputs(q, k, v, slopes) -> None:
+    """The reference's checks (co_alibi_attn.py:30-33, AssertionError) plus the kernels'
+    dtype (TypeError) and head-dim (ValueError) limits."""
+    batch_size, num_heads, _, head_dim = q.shape
     num_kv_heads, seq_len_kv = k.shape[1], k.shape[2]
-
     assert num_kv_heads >= 1 and num_heads % num_kv_heads == 0
     assert k.shape == (batch_size, num_kv_heads, seq_len_kv, head_dim)
     assert v.shape == (batch_size, num_kv_heads, seq_len_kv, head_dim)
@@ -73,69 +58,30 @@ def _forward(q, k, v, slopes, causal, sm_scale, with_stats: bool):
         raise TypeError(f"q, k, v must share one dtype of float32/float16/bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
     _check_head_dim(head_dim, q.dtype)
 
-    q, k, v = _aligned(q), _aligned(k), _aligned(v)
-    slopes32 = slopes.detach().to(device=q.device, dtype=torch.float32).contiguous()
-    o = torch.empty_like(q)
-    lib = _native.lib()
-    lse = zb = None
-    if with_stats:
-        lse = torch.empty((batch_size, num_heads, seq_len_q), device=q.device, dtype=torch.float32)
-        zb = torch.empty(
-            lib.co_alibi_zb_numel(batch_size, num_heads, seq_len_q, seq_len_kv),
-            device=q.device,
-            dtype=torch.float32,
-        )
-    with torch.cuda.device(q.device):
-        _native.check(
-            lib.co_alibi_fwd(
-                _native.DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                slopes32.data_ptr(), o.data_ptr(), 0 if lse is None else lse.data_ptr(),
-                0 if zb is None else zb.data_ptr(),
-                batch_size, num_heads, num_kv_heads, seq_len_q, seq_len_kv, head_dim,
-                1 if causal else 0, float(sm_scale), _stream_handle(q.device),
-            )
-        )
-    return o, lse, zb, (q, k, v, slopes32)
-
 
 class CoALIBIAttention(torch.autograd.Function):
     """Autograd function over the native forward / backward (reference co_alibi_attn.py:24-135).
 
     ``apply(q, k, v, slopes, causal, sm_scale)``: q is (B, Hq, Sq, D); k and v
     are (B, Hkv, Skv, D) with Hq a multiple of Hkv (Hkv == Hq is the
-    reference's only form); slopes holds Hq penalty slopes.
+    reference's only form); slopes holds Hq penalty slopes.  The launches are the
+    operators ``co_alibi::fwd`` and ``co_alibi::bwd`` (co_alibi_attn/ops.py), which
+    ``co_alibi_attention`` calls directly.
     """
 
     @staticmethod
     def forward(ctx, q, k, v, slopes, causal, sm_scale):
-        o, lse, zb, (q, k, v, slopes32) = _forward(q, k, v, slopes, causal, sm_scale, with_stats=True)
-        ctx.save_for_backward(q, k, v, o, lse, zb, slopes32)
-        ctx.sm_scale = sm_scale
-        ctx.causal = causal
+        _check_inputs(q, k, v, slopes)
+        o, lse, zb = ops.fwd(q, k, v, slopes, bool(causal), float(sm_scale), True)
+        ctx.save_for_backward(q, k, v, o, lse, zb, slopes)
+        ctx.sm_scale = float(sm_scale)
+        ctx.causal = bool(causal)
         return o
 
     @staticmethod
     def backward(ctx, do):
-        q, k, v, o, lse, zb, slopes32 = ctx.saved_tensors
-        batch_size, num_heads, seq_len_q, head_dim = q.shape
-        num_kv_heads, seq_len_kv = k.shape[1], k.shape[2]
-        do = _aligned(do.to(q.dtype))
-        dq = torch.empty_like(q)
-        dk = torch.empty_like(k)
-        dv = torch.empty_like(v)
-        lib = _native.lib()
-        ws_bytes = lib.co_alibi_bwd_workspace_bytes(batch_size, num_heads, seq_len_q, seq_len_kv)
-        workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
-        with torch.cuda.device(q.device):
-            _native.check(
-                lib.co_alibi_bwd(
-                    _native.DTYPE_CODES[q.dtype], do.data_ptr(), q.data_ptr(), k.data_ptr(),
-                    v.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), slopes32.data_ptr(),
-                    dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), workspace.data_ptr(), ws_bytes,
-                    batch_size, num_heads, num_kv_heads, seq_len_q, seq_len_kv, head_dim,
-                    1 if ctx.causal else 0, float(ctx.sm_scale), _stream_handle(q.device),
-                )
-            )
+        q, k, v, o, lse, zb, slopes = ctx.saved_tensors
+        dq, dk, dv = ops.bwd(do, q, k, v, o, lse, zb, slopes, ctx.causal, ctx.sm_scale)
         return dq, dk, dv, None, None, None
 
 
@@ -146,19 +92,19 @@ def co_alibi_attention(q, k, v, causal=True, sm_scale=None, bias_max=8.0):
     head h uses key/value head h // (Hq // Hkv).  Returns (B, Hq, Sq, D) in
     q.dtype.  ``sm_scale`` defaults to D**-0.5; the per-head slope is twice the
     ALiBi slope of ``_get_coalibi_slopes(Hq, bias_max)``, rounded to q.dtype.
-    When no gradient can flow (grad mode off, or no input requires grad) the
-    forward runs without saving anything for a backward.
+    The launch is the operator ``co_alibi::fwd``, differentiable through
+    ``co_alibi::bwd``.  When no gradient can flow (grad mode off, or no input
+    requires grad) the forward neither allocates nor writes the statistics only the
+    backward reads.
     """
     if sm_scale is None:
         sm_scale = 1.0 / (q.shape[-1] ** 0.5)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     num_q_heads = q.shape[1]
     slopes = (2.0 * _get_coalibi_slopes(num_q_heads, bias_max)).to(q.device, dtype=q.dtype)
-    if not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)):
-        # Inference: no autograd record, and the statistics only the backward reads
-        # (LSE and the penalty block sums) are neither allocated nor written.
-        return _forward(q, k, v, slopes, causal, sm_scale, with_stats=False)[0]
-    return CoALIBIAttention.apply(q, k, v, slopes, causal, sm_scale)
+    _check_inputs(q, k, v, slopes)
+    needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+    return ops.fwd(q, k, v, slopes, bool(causal), float(sm_scale), needs_grad)[0]
 
 
 def co_alibi_decode(q, k_cache, v_cache, seq_len=None, sm_scale=None, bias_max=8.0, return_lse=False,
@@ -207,21 +153,7 @@ def co_alibi_decode(q, k_cache, v_cache, seq_len=None, sm_scale=None, bias_max=8
     if sm_scale is None:
         sm_scale = 1.0 / (head_dim ** 0.5)
 
-    q, k_cache, v_cache = _aligned(q.detach()), _aligned(k_cache.detach()), _aligned(v_cache.detach())
     slopes = (2.0 * _get_coalibi_slopes(num_heads, bias_max)).to(q.device, dtype=q.dtype)
-    slopes32 = slopes.to(torch.float32).contiguous()
-    o = torch.empty_like(q)
-    lse = torch.empty((batch_size, num_heads, 1), device=q.device, dtype=torch.float32) if return_lse else None
-    lib = _native.lib()
-    ws_bytes = lib.co_alibi_decode_workspace_bytes(batch_size, num_heads, bound, head_dim)
-    workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
-    with torch.cuda.device(q.device):
-        _native.check(
-            lib.co_alibi_decode(
-                _native.DTYPE_CODES[q.dtype], q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                slopes32.data_ptr(), 0 if lens is None else lens.data_ptr(), o.data_ptr(),
-                0 if lse is None else lse.data_ptr(), workspace.data_ptr(), ws_bytes, batch_size, num_heads,
-                num_kv_heads, bound, capacity, head_dim, float(sm_scale), _stream_handle(q.device),
-            )
-        )
+    o, lse = ops.decode(q.detach(), k_cache.detach(), v_cache.detach(), slopes, lens, bound, float(sm_scale),
+                        bool(return_lse))
     return (o, lse) if return_lse else o
