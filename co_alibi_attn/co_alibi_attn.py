@@ -37,6 +37,26 @@ def _get_coalibi_slopes(n_heads: int, bias_max: float = 8.0) -> torch.Tensor:
     return slopes.abs()
 
 
+_DEVICE_SLOPES: dict = {}
+
+
+def _device_slopes(n_heads: int, bias_max: float, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """The penalty slopes 2 * _get_coalibi_slopes(n_heads, bias_max) rounded to ``dtype`` on
+    ``device`` (reference co_alibi_attn.py:147), kept per (n_heads, bias_max, dtype, device):
+    a copy from pageable host memory synchronises the stream, which would drain the GPU's
+    queue at every call and make a graph capture fail.  Under torch.compile the values are
+    computed in the traced graph instead."""
+    if torch.compiler.is_compiling():
+        return (2.0 * _get_coalibi_slopes(n_heads, bias_max)).to(device, dtype=dtype)
+    key = (int(n_heads), float(bias_max), dtype, torch.device(device))
+    slopes = _DEVICE_SLOPES.get(key)
+    if slopes is None:
+        slopes = (2.0 * _get_coalibi_slopes(n_heads, bias_max)).to(device, dtype=dtype)
+        if type(slopes) is torch.Tensor:  # not a FakeTensor made under a tracing mode
+            _DEVICE_SLOPES[key] = slopes
+    return slopes
+
+
 def _check_head_dim(head_dim: int, dtype: torch.dtype) -> None:
     if head_dim not in _native.SUPPORTED_HEAD_DIMS:
         raise ValueError(f"head_dim must be one of {_native.SUPPORTED_HEAD_DIMS}, got {head_dim}")
@@ -101,7 +121,7 @@ def co_alibi_attention(q, k, v, causal=True, sm_scale=None, bias_max=8.0):
         sm_scale = 1.0 / (q.shape[-1] ** 0.5)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     num_q_heads = q.shape[1]
-    slopes = (2.0 * _get_coalibi_slopes(num_q_heads, bias_max)).to(q.device, dtype=q.dtype)
+    slopes = _device_slopes(num_q_heads, bias_max, q.dtype, q.device)
     _check_inputs(q, k, v, slopes)
     needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
     return ops.fwd(q, k, v, slopes, bool(causal), float(sm_scale), needs_grad)[0]
@@ -153,7 +173,7 @@ def co_alibi_decode(q, k_cache, v_cache, seq_len=None, sm_scale=None, bias_max=8
     if sm_scale is None:
         sm_scale = 1.0 / (head_dim ** 0.5)
 
-    slopes = (2.0 * _get_coalibi_slopes(num_heads, bias_max)).to(q.device, dtype=q.dtype)
+    slopes = _device_slopes(num_heads, bias_max, q.dtype, q.device)
     o, lse = ops.decode(q.detach(), k_cache.detach(), v_cache.detach(), slopes, lens, bound, float(sm_scale),
                         bool(return_lse))
     return (o, lse) if return_lse else o

@@ -122,3 +122,41 @@ def test_graph_capture_replays_match_eager():
         for name, got, ref in zip(("o", "lse", "dq", "dk", "dv", "decode o", "decode lse"), outs, want):
             assert torch.equal(got, ref), f"replay {rep}: {name} differs from eager"
         print(f"  replay {rep} matches eager", flush=True)
+
+
+@pytest.mark.filterwarnings("ignore:The AccumulateGrad node's stream")  # leaves first used on the warm-up stream
+def test_public_function_captures_in_a_graph():
+    """After one eager call (which puts the slopes on the device), co_alibi_attention and its
+    backward through torch.autograd.grad capture into a graph: the public path has no host
+    synchronisation.  Replays with new inputs equal eager."""
+    print("graph capture of co_alibi_attention", flush=True)
+    B, Hq, Hkv, S, D, dt = 2, 8, 4, 200, 64, torch.bfloat16
+    q, k, v, do = make(B, Hq, Hkv, S, D, dt, seed=20)
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+
+    def step():
+        o = co_alibi_attention(*leaves)
+        return (o, *torch.autograd.grad(o, leaves, do))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    for rep in range(2):
+        nq, nk, nv, ndo = make(B, Hq, Hkv, S, D, dt, seed=200 + rep)
+        with torch.no_grad():
+            for dst, src in zip((*leaves, do), (nq, nk, nv, ndo)):
+                dst.copy_(src)
+        torch.cuda.synchronize()
+        want = step()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, ref in zip(("o", "dq", "dk", "dv"), outs, want):
+            assert torch.equal(got, ref), f"replay {rep}: {name} differs from eager"

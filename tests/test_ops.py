@@ -89,3 +89,15 @@ def test_public_functions_trace_under_fake_tensors():
         assert o.shape == (2, 12, 1, 64) and lse.shape == (2, 12, 1)
         with pytest.raises(AssertionError):  # 12 query heads cannot share 5 key heads
             co_alibi_attn.co_alibi_attention(q, kv[:, :1].expand(2, 5, 40, 64), kv[:, :1].expand(2, 5, 40, 64))
+
+
+def test_slopes_are_kept_per_device_and_never_fake():
+    """The device slopes are built once per (heads, bias_max, dtype, device), equal the
+    reference formula rounded to the dtype, and a FakeTensor made while tracing is not kept."""
+    from co_alibi_attn.co_alibi_attn import _DEVICE_SLOPES, _device_slopes, _get_coalibi_slopes
+    a = _device_slopes(12, 8.0, torch.bfloat16, torch.device("cpu"))
+    assert a is _device_slopes(12, 8.0, torch.bfloat16, torch.device("cpu"))
+    assert torch.equal(a, (2.0 * _get_coalibi_slopes(12, 8.0)).to(torch.bfloat16))
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        _device_slopes(6, 4.0, torch.float16, torch.device("cuda", 0))
+    assert (6, 4.0, torch.float16, torch.device("cuda", 0)) not in _DEVICE_SLOPES
