@@ -15,6 +15,10 @@ benchmark:
   python3 co_alibi_attn/profiling.py traffic FETCH_DIR WRITE_DIR --command CMD --out FILE
       HBM bytes per launch from a ``--pmc FETCH_SIZE`` and a ``--pmc WRITE_SIZE``
       pass, each scaled by what the same counter reads for the calibration copy
+  python3 co_alibi_attn/profiling.py counters DIR_A DIR_B --command CMD --out FILE
+      per-kernel shader counters (MFMA and VALU busy, instruction mix, LDS bank
+      conflicts) from the two ``--pmc`` passes of COUNTER_PASSES, with the HBM
+      rate from the traffic and duration summaries when they are given
 
 Flop accounting.  The algorithmic work is the FlashAttention convention:
 forward 2 products (QK^T, PV) and backward 5 (S, dS, dV, dQ, dK), each
@@ -41,6 +45,15 @@ CALIBRATION_BYTES = 1 << 30
 KERNELS = ("coalibi_fwd_kernel", "coalibi_bwd_dq_kernel", "coalibi_bwd_dkdv_kernel")
 DECODE_KERNELS = ("coalibi_decode_split_kernel", "coalibi_decode_merge_kernel")
 NAMED_KERNELS = KERNELS + DECODE_KERNELS
+# The two --pmc passes of the counter summary: at most 8 SQ and 2 GRBM counters each.
+COUNTER_PASSES = (
+    ("SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU", "SQ_WAVES",
+     "SQ_WAVE_CYCLES", "GRBM_GUI_ACTIVE"),
+    ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS", "SQ_LDS_BANK_CONFLICT",
+     "SQ_ACTIVE_INST_ANY", "SQ_WAIT_INST_LDS", "SQ_BUSY_CU_CYCLES", "GRBM_GUI_ACTIVE"),
+)
+MI355X_CUS = 256   # 4 SIMDs each
+MI355X_XCDS = 8    # GRBM_GUI_ACTIVE is read once per XCD
 # (charged, issued) products per launch, in units of one GEMM of 2*B*Hq*D flops per visible pair.
 PRODUCTS = {"coalibi_fwd_kernel": (2, 2), "coalibi_bwd_dq_kernel": (1, 3), "coalibi_bwd_dkdv_kernel": (4, 4)}
 
@@ -312,6 +325,92 @@ def cmd_traffic(args) -> None:
     _write(args.out, lines)
 
 
+def _counters_per_dispatch(directory: str):
+    """{kernel: {counter: mean over dispatches of the value summed over its instances}}."""
+    acc = defaultdict(float)
+    names = {}
+    for r in _csv_rows(directory, "counter_collection.csv"):
+        key = (r["Process_Id"], r["Dispatch_Id"], r["Counter_Name"])
+        acc[key] += float(r["Counter_Value"])
+        names[key[:2]] = r["Kernel_Name"]
+    per = defaultdict(lambda: defaultdict(list))
+    for (pid, did, counter), val in acc.items():
+        per[_short(names[(pid, did)])][counter].append(val)
+    return {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in per.items()}
+
+
+def _stats_average_us(path: str):
+    """{kernel: average duration in us} from a summary written by ``stats``."""
+    out = {}
+    if path and os.path.exists(path):
+        with open(path) as fh:
+            for line in fh:
+                cells = [c.strip() for c in line.split("|")]
+                if len(cells) > 4 and cells[1].startswith("`"):
+                    out[cells[1].strip("`")] = float(cells[3])
+    return out
+
+
+def cmd_counters(args) -> None:
+    """Shader counters per kernel.  Normalisation (MI355X: 256 CUs, 1024 SIMDs, 8 XCDs):
+    - active cycles per dispatch T = GRBM_GUI_ACTIVE / 8 (the counter is summed over the XCDs);
+    - MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 T) (summed over SIMDs);
+    - VALU busy = 4 SQ_ACTIVE_INST_VALU / (1024 T) (quad-cycles summed over waves; one VALU
+      instruction issues per SIMD and cycle, so this is the SIMDs' VALU-issue share);
+    - LDS bank conflicts: SQ_LDS_BANK_CONFLICT cycles per LDS instruction and as a share of
+      the cycles the LDS instructions were active (4 SQ_ACTIVE_INST_LDS);
+    - HBM rate = traffic bytes per launch / average duration, from the traffic and stats
+      summaries."""
+    merged = defaultdict(dict)
+    for d in args.dirs:
+        for k, cs in _counters_per_dispatch(d).items():
+            for c, v in cs.items():
+                merged[k].setdefault(c, []).append(v)
+    data = {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in merged.items()}
+    traffic = read_traffic(args.traffic) if args.traffic else {}
+    durations = _stats_average_us(args.stats)
+    simds = 4 * MI355X_CUS
+    lines = [f"# Shader counters per launch: {args.title}", "", "Commands (R is the repository root on the GPU box):",
+             "", "```", args.command, "```", "",
+             "The summary is written by `python3 co_alibi_attn/profiling.py counters <pass dirs>`. Definitions "
+             "(MI355X: 256 CUs = 1024 SIMDs, 8 XCDs; T = GRBM_GUI_ACTIVE / 8, the active cycles of a dispatch):",
+             "",
+             "- MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 T);",
+             "- VALU busy = 4 SQ_ACTIVE_INST_VALU / (1024 T), the SIMDs' VALU-issue share;",
+             "- instruction mix = SQ_INSTS_* per SQ_INSTS_MFMA;",
+             "- LDS conflict = SQ_LDS_BANK_CONFLICT cycles per SQ_INSTS_LDS, and as a share of 4 SQ_ACTIVE_INST_LDS;",
+             "- HBM GB/s = traffic per launch (`profiles/traffic_*.md`) / average duration "
+             "(`profiles/kernel_stats_*.md`).", "",
+             "| kernel | MFMA busy | VALU busy | VALU / MFMA | trans / MFMA | LDS / MFMA | LDS conflict cycles / LDS instr "
+             "| conflict share of LDS cycles | HBM GB/s |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for k in NAMED_KERNELS:
+        if k not in data:
+            continue
+        c = data[k]
+        t = c.get("GRBM_GUI_ACTIVE", 0.0) / MI355X_XCDS
+        mf = c.get("SQ_INSTS_MFMA", 0.0)
+        def frac(x):
+            return f"{100.0 * x:.1f} %"
+        mfma_busy = frac(c["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * t)) if t and "SQ_VALU_MFMA_BUSY_CYCLES" in c else "-"
+        valu_busy = frac(4 * c["SQ_ACTIVE_INST_VALU"] / (simds * t)) if t and "SQ_ACTIVE_INST_VALU" in c else "-"
+        def per_mfma(name):
+            return f"{c[name] / mf:.2f}" if mf and name in c else "-"
+        lds = c.get("SQ_INSTS_LDS", 0.0)
+        conf = c.get("SQ_LDS_BANK_CONFLICT")
+        conf_per = f"{conf / lds:.3f}" if conf is not None and lds else "-"
+        lds_cyc = 4 * c.get("SQ_ACTIVE_INST_LDS", 0.0)
+        conf_share = frac(conf / lds_cyc) if conf is not None and lds_cyc else "-"
+        hbm = (f"{traffic[k] / (durations[k] * 1e-6) / 1e9:.0f}" if k in traffic and durations.get(k) else "-")
+        lines.append(f"| `{k}` | {mfma_busy} | {valu_busy} | {per_mfma('SQ_INSTS_VALU')} | "
+                     f"{per_mfma('SQ_INSTS_VALU_TRANS_F32')} | {per_mfma('SQ_INSTS_LDS')} | {conf_per} | {conf_share} | {hbm} |")
+    lines += ["", "Raw means per dispatch:", ""]
+    for k in NAMED_KERNELS:
+        if k in data:
+            lines.append(f"- `{k}`: " + ", ".join(f"{c} {v:.4g}" for c, v in sorted(data[k].items())))
+    _write(args.out, lines)
+
+
 def read_traffic(path: str):
     """{kernel: HBM bytes per launch} from a summary written by ``traffic`` (empty if the file is absent)."""
     out = {}
@@ -352,8 +451,15 @@ def main(argv=None) -> None:
     t.add_argument("--command", required=True)
     t.add_argument("--title", default="headline workload")
     t.add_argument("--out", default="-")
+    c = sub.add_parser("counters")
+    c.add_argument("dirs", nargs="+")
+    c.add_argument("--command", required=True)
+    c.add_argument("--title", default="headline workload")
+    c.add_argument("--traffic", default=None, help="summary written by traffic (for the HBM rate)")
+    c.add_argument("--stats", default=None, help="summary written by stats (average durations)")
+    c.add_argument("--out", default="-")
     args = ap.parse_args(argv)
-    {"run": cmd_run, "stats": cmd_stats, "traffic": cmd_traffic}[args.cmd](args)
+    {"run": cmd_run, "stats": cmd_stats, "traffic": cmd_traffic, "counters": cmd_counters}[args.cmd](args)
 
 
 if __name__ == "__main__":
