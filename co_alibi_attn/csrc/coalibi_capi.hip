@@ -262,6 +262,11 @@ size_t decode_chunks(int seq_kv) {
   return (static_cast<size_t>(seq_kv) + coalibi::kDecodeChunkKeys - 1) / coalibi::kDecodeChunkKeys;
 }
 
+// Upper bound of the split count of a decode over seq_kv keys (one split holds >= 1 chunk).
+size_t decode_splits_max(int seq_kv) {
+  return std::min(decode_chunks(seq_kv), static_cast<size_t>(coalibi::kMaxDecodeSplits));
+}
+
 // Compute units of the current device (queried once per device).
 int device_cus() {
   static std::atomic<int> cached[64];
@@ -281,7 +286,7 @@ extern "C" {
 
 size_t co_alibi_decode_workspace_bytes(int batch, int heads_q, int seq_kv, int head_dim) {
   if (batch < 1 || heads_q < 1 || seq_kv < 1 || head_dim < 1) return 0;
-  const size_t parts = static_cast<size_t>(batch) * heads_q * decode_chunks(seq_kv);
+  const size_t parts = static_cast<size_t>(batch) * heads_q * decode_splits_max(seq_kv);
   return 3 * round_up(parts * sizeof(float), 256) + parts * head_dim * sizeof(float);
 }
 
@@ -311,7 +316,7 @@ int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v
                                      " bytes, need " + std::to_string(need));
   if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": sm_scale must be finite");
 
-  const size_t parts = static_cast<size_t>(batch) * heads_q * decode_chunks(seq_kv);
+  const size_t parts = static_cast<size_t>(batch) * heads_q * decode_splits_max(seq_kv);
   const size_t stat_bytes = round_up(parts * sizeof(float), 256);
   char* ws = static_cast<char*>(workspace);
   coalibi::DecodeArgs a{};
@@ -336,7 +341,7 @@ int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v
   // Enough splits to give every CU kDecodeWGsPerCU work-groups; each walks cps chunks.
   const long long units = static_cast<long long>(batch) * heads_kv;
   const long long want = (static_cast<long long>(coalibi::kDecodeWGsPerCU) * device_cus() + units - 1) / units;
-  const int splits = static_cast<int>(std::max(1LL, std::min<long long>(want, a.nChunks)));
+  const int splits = static_cast<int>(std::max(1LL, std::min<long long>(want, decode_splits_max(seq_kv))));
   a.cps = (a.nChunks + splits - 1) / splits;
   a.nSplits = (a.nChunks + a.cps - 1) / a.cps;
   a.sc2 = sm_scale * coalibi::kLog2eHost;

@@ -7,21 +7,23 @@
 //   O   = sum_j 2^(a_j - m) v_j / sum_j 2^(a_j - m),   LSE = (m + log2 l) * ln 2.
 //
 // Decode reads the whole cache once for O(L*D) flops per query head: it is bound by
-// HBM bandwidth.  The keys are split into chunks of 256 (split-K) so that every CU
-// streams a part of the cache, and two kernels run:
-//   1. split: per (chunk, batch, kv head), all query heads of the group at once.
-//      S^T = K_chunk Q^T on MFMA (keys on the accumulator rows, the group's query
-//      heads on the columns), z from the sigma suffix inside the chunk only, the
-//      chunk's softmax partial (max, sum, O = P V on MFMA) and its sigma total.
+// HBM bandwidth.  The keys form chunks of 128 (one 32-key tile per wavefront), and
+// runs of chunks (splits) go to separate work-groups so that every CU streams a part of
+// the cache.  Two kernels run:
+//   1. split: per (split, batch, kv head), all query heads of the group at once, chunks
+//      from the split's last to its first.  S^T = K_chunk Q^T on MFMA (keys on the
+//      accumulator rows, the group's query heads on the columns), z from the sigma
+//      suffix inside the split only, the split's softmax partial (max, sum, O = P V on
+//      MFMA) and its sigma total.
 //   2. merge: per (batch, query head).  The keys after chunk c add the same amount
 //      off_c = sum_{c' > c} sigma_total[c'] to z_j of every key of chunk c, which
 //      shifts a_j of the whole chunk by -slope*log2(e)*off_c and leaves its sum and
 //      O partial unchanged once the maximum is shifted by the same amount.  The
-//      merge therefore scans the chunk sigma totals, shifts the chunk maxima and
+//      merge therefore scans the split sigma totals, shifts the split maxima and
 //      combines the partials with the usual rescaling.
-// K is read straight into MFMA fragments with buffer loads; V goes to LDS by
-// buffer-to-LDS DMA, issued first so that it overlaps the score products, and is read
-// back as the k-major B operand of P V.
+// K and V go to per-wavefront LDS tiles by buffer-to-LDS DMA, each issued one chunk ahead
+// as soon as its tile has been read; K is read back as the MFMA A operand, V as the k-major
+// B operand of P V.
 #include "coalibi_common.h"
 #include "coalibi_kernels.h"
 
@@ -30,31 +32,50 @@ namespace coalibi {
 namespace {
 
 constexpr int kDecWaves = 4;
-constexpr int kDecWaveKeys = 64;                      // keys per wavefront: two 32-key MFMA tiles
+constexpr int kDecWaveKeys = 32;  // keys per wavefront: one 32-key MFMA tile
 constexpr int kDecMergeThreads = 256;
 static_assert(kDecWaves * kDecWaveKeys == kDecodeChunkKeys, "chunk = the work-group's keys");
 
 template <typename T, int D>
 struct DecCfg {
-  // V row stride in LDS (elements): the transpose-read layout of the forward for 16-bit,
-  // one 16-byte pad for fp32 (read element-wise).
-  static constexpr int LD = sizeof(T) == 2 ? D + 16 : D + 4;
+  static constexpr bool kTr = sizeof(T) == 2;
+  static constexpr int CH = 16 / (int)sizeof(T);
+  // LDS row strides (elements).  K rows are read as MFMA A operands with 16-byte row reads,
+  // which a stride of 4 (mod 8) dwords keeps on distinct banks within a read pass.  V rows
+  // are read k-major: 16-bit transpose reads (4 rows x 64 bytes a pass) are conflict-free at
+  // a stride of 16 (mod 32) dwords; fp32 reads V element by element.
+  static constexpr int LDK = D + CH;
+  static constexpr int LDV = kTr ? D + 2 * ((48 - (D / 2) % 32) % 32) : D + CH;
+  using KTile = DmaTile<T, D, kDecWaveKeys, LDK, 1, true>;
+  using VTile = DmaTile<T, D, kDecWaveKeys, LDV, 1, false>;
+  static constexpr int K_ELEMS = KTile::LDS_ELEMS;  // a wavefront's K tile
+  static constexpr int V_ELEMS = VTile::LDS_ELEMS;  // a wavefront's V tile
   static constexpr int KS = D / 16;  // k16 steps over the head dim
   static constexpr int DT = D / 32;  // 32-column tiles of O
-  static constexpr int WAVE_ELEMS = kDecWaveKeys * LD;
-  static_assert(kMaxDecodeGroup * D * 4 <= WAVE_ELEMS * (int)sizeof(T), "O partials alias the V tile");
+  // At the end the O partials of heads 0..15 alias a wavefront's K tile, of heads 16..31 its V tile.
+  static_assert(kMaxDecodeGroup / 2 * D * 4 <= K_ELEMS * (int)sizeof(T) &&
+                    kMaxDecodeGroup / 2 * D * 4 <= V_ELEMS * (int)sizeof(T),
+                "O partials alias the tiles");
 };
 
-// Eight consecutive elements of a row of T through a buffer resource.
-template <typename T>
-__device__ __forceinline__ typename Mfma<T>::vec8 buf_vec8(__amdgpu_buffer_rsrc_t r, int byte_off) {
-  if constexpr (sizeof(T) == 2) {
-    return __builtin_bit_cast(typename Mfma<T>::vec8, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
-  } else {
-    typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
-    const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
-    const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off + 16, 0, 0);
-    return __builtin_bit_cast(f32x8, u32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+// Buffer-to-LDS DMA of the kDecWaveKeys rows row0.. of a row-major [nrows][D] matrix into
+// one wavefront's tile (the layout of DmaTile<T, D, kDecWaveKeys, LD, 1, PERM>): every
+// instruction reads 64 consecutive 16-byte chunks, non-temporal (the cache is read once per
+// step).  Rows past nrows, pad chunks and the tail after the last row land as zeros.  The source offsets are recomputed from an opaque
+// copy of the lane index at every issue; hoisted out of the chunk loop they would hold a
+// register per instruction for the whole kernel.
+template <typename T, int D, int LD, bool PERM>
+__device__ __forceinline__ void dma_wave_rows(const T* base, int row0, int nrows, T* lds, int lane) {
+  using Tile = DmaTile<T, D, kDecWaveKeys, LD, 1, PERM>;
+  const __amdgpu_buffer_rsrc_t r = tile_rsrc(base + (size_t)row0 * D, min(max(nrows - row0, 0), kDecWaveKeys) * D);
+  int ln;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
+#pragma unroll
+  for (int m = 0; m < Tile::NINSTR; ++m) {
+    const int ch = m * 64 + ln, row = ch / Tile::CPR, j = ch - row * Tile::CPR;
+    const int src = PERM ? (row & ~31) + kRowOfReg(row & 31) : row;
+    const bool in_tile = row < kDecWaveKeys && j < D / Tile::CH;
+    dma16_to_lds_nt(r, lds + m * 64 * Tile::CH, in_tile ? (src * D + j * Tile::CH) * (int)sizeof(T) : 0x40000000);
   }
 }
 
@@ -74,20 +95,54 @@ __device__ __forceinline__ typename Mfma<T>::vec8 ld_kmajor_dec(const T* tile, i
   }
 }
 
-// s_waitcnt immediate that waits until at most n vector-memory operations are outstanding
-// and leaves the LDS / export counters alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
+// The KS fragments (16 bytes each, 32 bytes apart) of one K row of a 16-bit tile, read by
+// inline assembly, four per statement, each statement waiting for its own reads before its
+// results are used.  Compiled LDS reads of the tile would make the compiler wait, before
+// them, for every buffer-to-LDS DMA in flight, the V tile's included; the explicit vmcnt
+// waits of the chunk loop already order these reads after the K tile's DMA.
+template <typename T, int KS>
+__device__ __forceinline__ void ld_k_fragments(typename Mfma<T>::vec8 (&f)[KS], const T* row) {
+  static_assert(sizeof(T) == 2 && KS % 2 == 0, "16-bit tiles, an even number of fragments");
+  const unsigned a = (unsigned)(size_t)(const __attribute__((address_space(3))) T*)row;  // LDS byte address
+  u32x4 u[KS];
+#pragma unroll
+  for (int g = 0; g + 4 <= KS; g += 4)
+    asm volatile(
+        "ds_read_b128 %0, %4 offset:%5\n\t"
+        "ds_read_b128 %1, %4 offset:%6\n\t"
+        "ds_read_b128 %2, %4 offset:%7\n\t"
+        "ds_read_b128 %3, %4 offset:%8\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(u[g]), "=&v"(u[g + 1]), "=&v"(u[g + 2]), "=&v"(u[g + 3])
+        : "v"(a), "i"(32 * g), "i"(32 * (g + 1)), "i"(32 * (g + 2)), "i"(32 * (g + 3))
+        : "memory");
+  if constexpr (KS % 4 == 2)
+    asm volatile(
+        "ds_read_b128 %0, %2 offset:%3\n\t"
+        "ds_read_b128 %1, %2 offset:%4\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(u[KS - 2]), "=&v"(u[KS - 1])
+        : "v"(a), "i"(32 * (KS - 2)), "i"(32 * (KS - 1))
+        : "memory");
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) f[ks] = __builtin_bit_cast(typename Mfma<T>::vec8, u[ks]);
+}
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt
+// 11:8): at most n vector-memory operations outstanding, or no LDS operation outstanding.
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kLgkmcnt0 = 15 | (3 << 14) | (7 << 4);
 
 template <typename T, int D>
-__global__ __launch_bounds__(kDecWaves * 64, D > 128 ? 1 : 2) void coalibi_decode_split_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kDecWaves * 64, (D > 128 || sizeof(T) == 4) ? 1 : 2) void coalibi_decode_split_kernel(
+    DecodeArgs a) {
   using M = Mfma<T>;
   using V8 = typename M::vec8;
   using C = DecCfg<T, D>;
-  constexpr int kKLoads = 2 * C::KS * (sizeof(T) == 4 ? 2 : 1);  // buffer loads per K fragment set
-  // The next chunk's K loads during this chunk's math; at D = 256 its registers do not
-  // fit beside the chunk state and it is loaded after P V instead.
-  constexpr bool kPrefetch = D <= 128;
-  __shared__ __align__(16) T sV[kDecWaves * C::WAVE_ELEMS];
+  // K tiles, V tiles and the exchange arrays are separate objects: the compiler then knows
+  // that reading one does not race the DMA into another, and adds no wait for it.
+  __shared__ __align__(16) T sK[kDecWaves * C::K_ELEMS];
+  __shared__ __align__(16) T sV[kDecWaves * C::V_ELEMS];
   __shared__ float sSig[2][kDecWaves][kMaxDecodeGroup];  // per-wavefront sigma totals (by chunk parity)
   __shared__ float sMax[kDecWaves][kMaxDecodeGroup];
   __shared__ float sSum[kDecWaves][kMaxDecodeGroup];
@@ -117,42 +172,24 @@ __global__ __launch_bounds__(kDecWaves * 64, D > 128 ? 1 : 2) void coalibi_decod
   }
   const T* const kbase = static_cast<const T*>(a.k) + (size_t)bhk * a.cap * D;
   const T* const vbase = static_cast<const T*>(a.v) + (size_t)bhk * a.cap * D;
-  T* const sVw = sV + wave * C::WAVE_ELEMS;
+  T* const sKw = sK + wave * C::K_ELEMS;  // this wavefront's tiles
+  T* const sVw = sV + wave * C::V_ELEMS;
   const bool head_ok = hl < G;
   const int hsafe = head_ok ? hl : 0;
   const float lam2 = a.slopes[hq0 + hsafe] * kLog2e;
 
-  // K fragments of chunk c: A row R of tile i holds key 32*i + kRowOfReg(R), so register r
-  // of lane l ends up with key 32*i + 16*(l/32) + r of the wavefront.  Keys past L read 0.
-  auto load_k_tile = [&](V8 (&dst)[C::KS], int c, int i) {
-    const int row0 = c * kDecodeChunkKeys + wave * kDecWaveKeys;
-    const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kbase + (size_t)row0 * D, min(max(L - row0, 0), kDecWaveKeys) * D);
-#pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks)
-      dst[ks] = buf_vec8<T>(kr, ((32 * i + kRowOfReg(hl)) * D + ks * 16 + hh * 8) * (int)sizeof(T));
+  // Both tiles of a chunk come in by DMA (whole 16-byte chunks of consecutive rows: per-lane
+  // fragment loads straight from HBM touch 32 rows per instruction and stream at about half
+  // the rate).  K rows are permuted (LDS row R holds key kRowOfReg(R)) so that register r of
+  // lane l of S^T holds key 16*(l/32) + r of the wavefront.
+  auto issue_k = [&](int c) {
+    dma_wave_rows<T, D, C::LDK, true>(kbase, c * kDecodeChunkKeys + wave * kDecWaveKeys, L, sKw, lane);
   };
-  // V rows row0.. of this wavefront -> its LDS tile by buffer-to-LDS DMA; each instruction
-  // writes 64 consecutive 16-byte chunks of the padded tile.  Pad chunks and rows past L
-  // point past the resource and land as zeros.  Offsets are recomputed per issue (they
-  // would otherwise hold a register per instruction for the whole kernel).
-  auto issue_v = [&](int row0) {
-    constexpr int CH = 16 / (int)sizeof(T), CPR = C::LD / CH, NINSTR = kDecWaveKeys * CPR / 64;
-    const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vbase + (size_t)row0 * D, min(max(L - row0, 0), kDecWaveKeys) * D);
-    // An opaque copy of the lane index keeps the offsets from being hoisted out of the
-    // chunk loop, where they would stay live (and spill) for the whole kernel.
-    int ln;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
-#pragma unroll
-    for (int m = 0; m < NINSTR; ++m) {
-      const int ch = m * 64 + ln, r = ch / CPR, j = ch - r * CPR;
-      dma16_to_lds(vr, sVw + m * 64 * CH, j < D / CH ? (r * D + j * CH) * (int)sizeof(T) : 0x40000000);
-    }
+  auto issue_v = [&](int c) {
+    dma_wave_rows<T, D, C::LDV, false>(vbase, c * kDecodeChunkKeys + wave * kDecWaveKeys, L, sVw, lane);
   };
-
-  V8 kf[2][C::KS];
-  load_k_tile(kf[0], c_last, 0);
-  load_k_tile(kf[1], c_last, 1);
-  issue_v(c_last * kDecodeChunkKeys + wave * kDecWaveKeys);
+  issue_k(c_last);
+  issue_v(c_last);
 
   // Q^T fragments: lane l holds query head l%32 of the group (zero past G).
   V8 qf[C::KS];
@@ -161,6 +198,9 @@ __global__ __launch_bounds__(kDecWaves * 64, D > 128 ? 1 : 2) void coalibi_decod
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) qf[ks] = head_ok ? ld_vec8(qrow + ks * 16) : zero_vec8<T>();
   }
+  // Wait for Q here, with the first chunk's tiles: the compiler would otherwise place this
+  // wait at its first use, inside the chunk loop, as a vmcnt(0) run on every chunk.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // Running state of this wavefront for the lane's head: maximum, sum, O (rows = heads).
   float m_run = kNegInf, l_run = 0.f, carry = 0.f;  // carry: sigma of the keys after this chunk
@@ -175,37 +215,40 @@ __global__ __launch_bounds__(kDecWaves * 64, D > 128 ? 1 : 2) void coalibi_decod
     const int row0 = c * kDecodeChunkKeys + wave * kDecWaveKeys;
     const bool more = c > c_first;
 
-    f32x16 sacc[2];
+    // This chunk's K has landed once at most its V (issued after it) is outstanding.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::VTile::NINSTR));
+    f32x16 sacc;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+    if constexpr (C::kTr) {
+      V8 kf[C::KS];
+      ld_k_fragments<T, C::KS>(kf, sKw + hl * C::LDK + hh * 8);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[i][r] = 0.f;
+      for (int ks = 0; ks < C::KS; ++ks) sacc = M::k16(kf[ks], qf[ks], sacc);
+    } else {
 #pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks) sacc[i] = M::k16(kf[i][ks], qf[ks], sacc[i]);
+      for (int ks = 0; ks < C::KS; ++ks) sacc = M::k16(ld_vec8(sKw + hl * C::LDK + ks * 16 + hh * 8), qf[ks], sacc);
     }
-    // The K fragments are consumed: the next chunk's load into them while this one finishes
-    // (tile 0 now, tile 1 before P V, which keeps 32 fewer registers live meanwhile).
-    if (kPrefetch && more) load_k_tile(kf[0], c - 1, 0);
+    // The K tile has been read: the next chunk's K lands in it during this chunk's math.
+    if (more) {
+      __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+      issue_k(c - 1);
+    }
 
-    // Scores and sigma.  Key order over the lanes: tile 0 half 0, tile 0 half 1, tile 1
-    // half 0, tile 1 half 1.  Keys past L get t = -inf: their sigma is 0 and their a and
-    // p follow as -inf and 0 without further masks.
-    // Sigma is summed here and recomputed in the suffix pass below rather than kept: the
-    // 32 registers it would hold are what keeps this kernel free of spills.
-    const int nvalid = L - (row0 + 16 * hh);  // register r of tile i is a key iff 32*i + r < nvalid
-    float tot[2] = {0.f, 0.f};
+    // Scores and sigma.  Keys past L get t = -inf: their sigma is 0 and their a and p
+    // follow as -inf and 0 without further masks.  Sigma is summed here and recomputed in
+    // the suffix pass below rather than kept in registers.
+    const int nvalid = L - (row0 + 16 * hh);  // register r is a key iff r < nvalid
+    float tot = 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        sacc[i][r] = 32 * i + r < nvalid ? sacc[i][r] * a.sc2 : kNegInf;
-        tot[i] += sigmoid_log2(sacc[i][r]);
-        asm volatile("" : "+v"(sacc[i][r]));  // opaque: the compiler would otherwise keep sigma live
-      }
-    const float oth0 = other_half(tot[0]), oth1 = other_half(tot[1]);
-    const float tile1 = tot[1] + oth1;
-    if (hh == 0 && head_ok) sSig[par][wave][hl] = tot[0] + oth0 + tile1;
-    __syncthreads();
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = r < nvalid ? sacc[r] * a.sc2 : kNegInf;
+      tot += sigmoid_log2(sacc[r]);
+      asm volatile("" : "+v"(sacc[r]));  // opaque: the compiler would otherwise keep sigma live
+    }
+    const float oth = other_half(tot);
+    if (hh == 0 && head_ok) sSig[par][wave][hl] = tot + oth;
+    lds_barrier();  // the DMA of the next chunk's K stays in flight
     // z offset of this wavefront: the keys of later wavefronts of the chunk, then of later chunks.
     float off = carry;
 #pragma unroll
@@ -216,15 +259,15 @@ __global__ __launch_bounds__(kDecWaves * 64, D > 128 ? 1 : 2) void coalibi_decod
     }
     par ^= 1;
 
+    // Suffix inside the tile: the lower half-wave's keys also see the upper half's total.
     float mx = kNegInf;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      float z = off + (hh == 0 ? (i == 0 ? oth0 : oth1) : 0.f) + (i == 0 ? tile1 : 0.f);
+    {
+      float z = off + (hh == 0 ? oth : 0.f);
 #pragma unroll
       for (int r = 15; r >= 0; --r) {
-        z += sigmoid_log2(sacc[i][r]);
-        sacc[i][r] -= lam2 * z;  // a; -inf stays -inf
-        mx = fmaxf(mx, sacc[i][r]);
+        z += sigmoid_log2(sacc[r]);
+        sacc[r] -= lam2 * z;  // a; -inf stays -inf
+        mx = fmaxf(mx, sacc[r]);
       }
     }
     mx = fmaxf(mx, other_half(mx));
@@ -236,21 +279,18 @@ __global__ __launch_bounds__(kDecWaves * 64, D > 128 ? 1 : 2) void coalibi_decod
     m_run = m_new;
 
     float lsum = 0.f;
-    V8 pa[2][2];
+    V8 pa[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int s = 0; s < 2; ++s) {
+      f32x8 pf;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        f32x8 pf;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int r = 8 * s + e;
-          const float p = fast_exp2(sacc[i][r] - mref);
-          pf[e] = p;
-          lsum += p;
-        }
-        pa[i][s] = M::pack(pf);
+      for (int e = 0; e < 8; ++e) {
+        const float p = fast_exp2(sacc[8 * s + e] - mref);
+        pf[e] = p;
+        lsum += p;
       }
+      pa[s] = M::pack(pf);
+    }
     l_run = l_run * fold + lsum + other_half(lsum);
     // O rows are query heads: register r of lane l holds head (r/4)*8 + (l/32)*4 + r%4.  The
     // factors go through this wavefront's LDS row (in-order LDS access within a wavefront).
@@ -264,27 +304,20 @@ __global__ __launch_bounds__(kDecWaves * 64, D > 128 ? 1 : 2) void coalibi_decod
         for (int j = 0; j < C::DT; ++j) oacc[j][4 * g + e] *= f[e];
     }
 
-    // V of this chunk has landed once at most the next chunk's K loads are outstanding.
-    if (kPrefetch && more) {
-      load_k_tile(kf[1], c - 1, 1);
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKLoads));
-    } else {
+    // This chunk's V has landed once at most the next chunk's K is outstanding.
+    if (more)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::KTile::NINSTR));
+    else
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    }
+    // O^T rows (heads) += P V: B operand rows are keys 8*s + 16*(l/32) + e, as in pa[s].
 #pragma unroll
     for (int j = 0; j < C::DT; ++j)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-          oacc[j] = M::k16(pa[i][s], ld_kmajor_dec<T>(sVw, C::LD, 32 * i + 8 * s, 16, 32 * j, lane), oacc[j]);
-
+      for (int s = 0; s < 2; ++s)
+        oacc[j] = M::k16(pa[s], ld_kmajor_dec<T>(sVw, C::LDV, 8 * s, 16, 32 * j, lane), oacc[j]);
     if (more) {
-      if constexpr (!kPrefetch) {
-        load_k_tile(kf[0], c - 1, 0);
-        load_k_tile(kf[1], c - 1, 1);
-      }
-      issue_v(row0 - kDecodeChunkKeys);
+      __builtin_amdgcn_s_waitcnt(kLgkmcnt0);  // the V tile has been read
+      issue_v(c - 1);
     }
   }
 
@@ -311,23 +344,27 @@ __global__ __launch_bounds__(kDecWaves * 64, D > 128 ? 1 : 2) void coalibi_decod
     a.psum[pi] = l;
     a.psig[pi] = carry;
   }
-  __syncthreads();  // sScale ready; every wavefront is done reading its V tile
+  __syncthreads();  // sScale ready; every wavefront is done with its tiles (no DMA in flight)
 
-  // Scaled O rows (query heads < G) into this wavefront's V region, then summed.
-  float* const sO = reinterpret_cast<float*>(sVw);
+  // Scaled O rows (query heads < G) into this wavefront's tiles (heads 0..15 the K tile,
+  // 16..31 the V tile), then summed over the wavefronts.
+  auto o_row = [&](int w, int h) {
+    return reinterpret_cast<float*>(h < kMaxDecodeGroup / 2 ? sK + w * C::K_ELEMS : sV + w * C::V_ELEMS) +
+           (h % (kMaxDecodeGroup / 2)) * D;
+  };
 #pragma unroll
   for (int j = 0; j < C::DT; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int h = (r >> 2) * 8 + hh * 4 + (r & 3);
-      if (h < G) sO[h * D + 32 * j + hl] = oacc[j][r] * sScale[wave][h];
+      if (h < G) o_row(wave, h)[32 * j + hl] = oacc[j][r] * sScale[wave][h];
     }
   __syncthreads();
   for (int i = tid; i < G * D; i += kDecWaves * 64) {
+    const int h = i / D, d = i - h * D;
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) s += reinterpret_cast<const float*>(sV + w * C::WAVE_ELEMS)[i];
-    const int h = i / D, d = i - h * D;
+    for (int w = 0; w < kDecWaves; ++w) s += o_row(w, h)[d];
     a.pout[((bh0 + h) * nS + split) * D + d] = s;
   }
 }
@@ -358,7 +395,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(kDecMergeThreads) void coalibi_decode_merge_kernel(DecodeArgs a) {
   constexpr int NW = kDecMergeThreads / 64;
   constexpr int PARTS = kDecMergeThreads / D;
-  __shared__ float sW[kMaxDecodeChunks];  // shifted split maxima, then split weights
+  __shared__ float sW[kMaxDecodeSplits];  // shifted split maxima, then split weights
   __shared__ float sRed[NW];
   __shared__ float sAcc[PARTS][D];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

@@ -50,9 +50,10 @@ struct BwdArgs {
 // keys form nChunks chunks of kDecodeChunkKeys; split s of a head covers chunks
 // [s*cps, (s+1)*cps).  Split-K partials per (b*Hq + h, split): pmax / psum / psig
 // (B*Hq, nSplits) and pout (B*Hq, nSplits, D), fp32.
-constexpr int kDecodeChunkKeys = 256;
+constexpr int kDecodeChunkKeys = 128;
 constexpr int kMaxDecodeGroup = 32;     // query heads per kv head (MFMA tile columns)
-constexpr int kMaxDecodeChunks = 8192;  // chunk weights held in LDS by the merge
+constexpr int kMaxDecodeChunks = 16384;  // bounds seq_kv (2^21 keys)
+constexpr int kMaxDecodeSplits = 1024;   // split partials per (batch, query head); merge weights in LDS
 
 struct DecodeArgs {
   const void* q;
@@ -70,8 +71,8 @@ struct DecodeArgs {
   float sc2;
 };
 
-// Split-K work-groups the decode aims at per CU (two are resident at a time).
-constexpr int kDecodeWGsPerCU = 4;
+// Split-K work-groups the decode aims at per CU: one round of the two that are resident.
+constexpr int kDecodeWGsPerCU = 2;
 
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);

@@ -90,7 +90,8 @@ int co_alibi_bwd_dkdv(int dtype, const void* dout, const void* q, const void* k,
                       int seq_q, int seq_kv, int head_dim, int causal, float sm_scale, void* stream);
 
 /* Bytes of device scratch co_alibi_decode needs: the split-K partials, 4 + head_dim
- * fp32 per (batch, query head, 256-key chunk). */
+ * fp32 per (batch, query head, split), for min(ceil(seq_kv / 128), 1024) splits (each
+ * split walks one or more 128-key chunks of the cache). */
 size_t co_alibi_decode_workspace_bytes(int batch, int heads_q, int seq_kv, int head_dim);
 
 /* Decode: one new query per (batch, query head) against a key / value cache.

@@ -113,10 +113,13 @@ def test_slopes_dtype_rounding():
 
 def test_decode_sizes():
     lib = _native.lib()
-    # 256-key chunks; per (b, h, chunk): max, sum, sigma total (each array 256-byte padded) + D floats
-    parts = 2 * 32 * 64  # B=2, Hq=32, 16384 keys
+    # min(ceil(L / 128), 1024) splits; per (b, h, split): max, sum, sigma total (each array
+    # 256-byte padded) + D floats
+    parts = 2 * 32 * 128  # B=2, Hq=32, 16384 keys
     assert lib.co_alibi_decode_workspace_bytes(2, 32, 16384, 128) == 3 * parts * 4 + parts * 128 * 4
-    assert lib.co_alibi_decode_workspace_bytes(1, 1, 257, 64) == 3 * 256 + 2 * 64 * 4
+    assert lib.co_alibi_decode_workspace_bytes(1, 1, 257, 64) == 3 * 256 + 3 * 64 * 4
+    parts = 1024  # 2^21 keys: 16384 chunks, at most 1024 splits
+    assert lib.co_alibi_decode_workspace_bytes(1, 1, 1 << 21, 64) == 3 * parts * 4 + parts * 64 * 4
     assert lib.co_alibi_decode_workspace_bytes(1, 1, 0, 64) == 0
 
 

@@ -48,7 +48,7 @@ def check(label, got, want, tol):
 # (B, Hq, Hkv, seq_len, capacity, D)
 CASES = [
     (1, 4, 4, 1, 1, 64),            # one key: O = v_0
-    (2, 8, 2, 300, 512, 128),       # group of 4, capacity > seq_len, second chunk 44 keys
+    (2, 8, 2, 300, 512, 128),       # group of 4, capacity > seq_len, last 128-key chunk 44 keys
     (1, 6, 2, 1000, 1000, 32),      # group of 3 (not a power of two)
     (1, 32, 1, 700, 768, 64),       # group of 32 (every MFMA column)
     (2, 16, 16, 257, 300, 128),     # no grouping, one key past a chunk
@@ -88,7 +88,8 @@ def test_decode_matches_oracle(case, dtype):
 
 
 def test_decode_long_cache_merges_many_chunks():
-    """70000 keys = 274 chunks: the merge's suffix scan of chunk sigma totals crosses its 256-chunk step."""
+    """70000 keys = 547 chunks of 128 in 183 splits of 3 chunks (on 256 CUs): every split walks several
+    chunks, carrying sigma across them, and the last one is partial."""
     B, Hq, Hkv, L, D = 1, 8, 2, 70000, 128
     q, k, v = cache_inputs(B, Hq, Hkv, L, L, D, torch.float16, seed=7)
     o, lse = co_alibi_decode(q.to(DEV), k.to(DEV), v.to(DEV), return_lse=True)
@@ -99,7 +100,8 @@ def test_decode_long_cache_merges_many_chunks():
 
 
 def test_decode_maximum_length():
-    """seq_len = 2^21, the largest accepted (8192 chunks, every merge weight held in LDS)."""
+    """seq_len = 2^21, the largest accepted: 16384 chunks in 512 splits (on 256 CUs), so the merge's
+    suffix scan of the split sigma totals crosses its 256-split step."""
     B, Hq, Hkv, L, D = 1, 2, 1, 1 << 21, 64
     q, k, v = cache_inputs(B, Hq, Hkv, L, L, D, torch.bfloat16, seed=11)
     o, lse = co_alibi_decode(q.to(DEV), k.to(DEV), v.to(DEV), return_lse=True)
