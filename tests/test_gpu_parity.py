@@ -310,6 +310,39 @@ def test_full_size_config(name):
             assert err <= TOL[w.dtype]
 
 
+@pytest.mark.parametrize("name", list(FULL))
+def test_full_size_invariances(name):
+    """Identities of the math at the BASELINE sizes, over every head (the oracle above samples a few):
+    - the backward is linear in dO: doubling dO doubles dQ, dK and dV (x2 is exact; the 16-bit
+      kernels round dP to the input type, so values in the subnormal range may move by an ulp);
+    - the softmax weights sum to 1 and D_i = dO_i.O_i absorbs the shift of dS_ij = dO_i.v_j, so a
+      constant added to V adds it to O and leaves dQ and dK unchanged, and dV bit for bit (nothing
+      dV reads depends on V)."""
+    w = WORKLOADS[name]
+    ulp = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[w.dtype]
+    print(f"invariances {name}: B{w.batch} Hq{w.heads_q} Hkv{w.heads_kv} S{w.seq} D{w.head_dim} {w.dtype}", flush=True)
+    q, k, v, do = make_inputs(w, seed=1)
+    run = lambda q_, k_, v_, do_: hip_fwd_bwd(q_, k_, v_, do_, causal=w.causal, bias_max=w.bias_max)  # noqa: E731
+    o, dq, dk, dv = run(q, k, v, do)
+    _, dq2, dk2, dv2 = run(q, k, v, (do.float() * 2).to(w.dtype))
+    for n_, a, b in (("dq", dq2, dq), ("dk", dk2, dk), ("dv", dv2, dv)):
+        excess = ((a - 2 * b).abs() - 2 * ulp * (2 * b).abs()).max().item()
+        print(f"  2 dO -> {n_}: largest error beyond 2 ulp {excess:.2e}", flush=True)
+        assert excess <= 1e-5, f"{n_} is not linear in dO"
+    c = 0.25
+    v_shift = (v.float() + c).to(w.dtype)
+    o3, dq3, dk3, dv3 = run(q, k, v_shift, do)
+    # v_shift - v is c up to the rounding of v + c (half an ulp of |v| + c), O up to its own rounding
+    shift = (o3 - o - c).abs().max().item()
+    print(f"  v + {c} -> o + {c}: max-abs {shift:.2e}", flush=True)
+    assert shift <= 8 * ulp
+    assert torch.equal(dv3, dv), "dV must not depend on V"
+    for n_, a, b in (("dq", dq3, dq), ("dk", dk3, dk)):
+        err = (a - b).abs().max().item()
+        print(f"  v + {c} -> {n_} unchanged: max-abs {err:.2e}", flush=True)
+        assert err <= TOL[w.dtype]
+
+
 # --------------------------------------------------------------------------- seeded random shapes
 
 def _random_cases(n=18, seed=2024):
