@@ -66,6 +66,14 @@ def fwd(q: Tensor, k: Tensor, v: Tensor, slopes: Tensor, causal: bool, sm_scale:
     are empty and the kernel writes neither."""
     batch, heads_q, seq_q, head_dim = q.shape
     heads_kv, seq_kv = k.shape[1], k.shape[2]
+    if q.numel() == 0 or seq_kv == 0:
+        # Nothing to launch.  Rows that see no key get what the reference's l = 0 gives:
+        # O = 0 / (0 + 1e-9) = 0 and LSE = -inf + log(1e-9) = -inf (co_alibi_fwd_kernel.py:115,120).
+        o = torch.zeros(q.shape, device=q.device, dtype=q.dtype)
+        if not with_stats:
+            return o, _empty_stats(q), _empty_stats(q)
+        lse = torch.full((batch, heads_q, seq_q), float("-inf"), device=q.device, dtype=torch.float32)
+        return o, lse, q.new_empty((zb_numel(batch, heads_q, seq_q, seq_kv),), dtype=torch.float32)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     slopes32 = slopes.detach().to(device=q.device, dtype=torch.float32).contiguous()
     o = torch.empty_like(q)
@@ -127,6 +135,8 @@ def bwd(do: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor, zb:
     input dtype; for Hkv < Hq dk / dv are summed over each group's query heads."""
     batch, heads_q, seq_q, head_dim = q.shape
     heads_kv, seq_kv = k.shape[1], k.shape[2]
+    if q.numel() == 0 or k.numel() == 0:  # no (query, key) pair: every gradient is zero
+        return tuple(torch.zeros(t.shape, device=t.device, dtype=t.dtype) for t in (q, k, v))
     q, k, v, o = _aligned(q), _aligned(k), _aligned(v), _aligned(o)
     do = _aligned(do.to(q.dtype))
     lse, zb = lse.contiguous(), zb.contiguous()
@@ -166,6 +176,10 @@ def decode(q: Tensor, k_cache: Tensor, v_cache: Tensor, slopes: Tensor, seq_lens
     natural-log LSE (B, Hq, 1) in fp32 (else an empty tensor)."""
     batch, heads_q, _, head_dim = q.shape
     heads_kv, capacity = k_cache.shape[1], k_cache.shape[2]
+    if q.numel() == 0:  # an empty batch
+        o = torch.empty(q.shape, device=q.device, dtype=q.dtype)
+        lse = torch.empty((batch, heads_q, 1), device=q.device, dtype=torch.float32) if with_lse else _empty_stats(q)
+        return o, lse
     q, k_cache, v_cache = _aligned(q), _aligned(k_cache), _aligned(v_cache)
     lens = None if seq_lens is None else seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
     slopes32 = slopes.detach().to(device=q.device, dtype=torch.float32).contiguous()

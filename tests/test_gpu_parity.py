@@ -20,6 +20,7 @@ import pytest
 import torch
 
 from co_alibi_attn import _native, co_alibi_attention
+from co_alibi_attn.co_alibi_attn import _get_coalibi_slopes
 from co_alibi_attn.workloads import WORKLOADS, make_inputs
 from oracle import co_alibi_ref as ref
 from tests.test_golden import GOLDEN, load_golden
@@ -267,6 +268,27 @@ def test_golden_fixtures(path):
     q, k, v, do = (t[n].to(dtype) for n in ("q", "k", "v", "do"))
     got = hip_fwd_bwd(q, k, v, do, causal=causal, sm_scale=sm_scale, bias_max=bias_max)
     assert_parity(got, (t["o"], t["dq"], t["dk"], t["dv"]), TOL[dtype], path.rsplit("/", 1)[-1], dtype)
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
+@pytest.mark.parametrize("shape", [(0, 4, 2, 64, 64), (2, 4, 2, 0, 64), (2, 4, 2, 64, 0)], ids=["B0", "Sq0", "Skv0"])
+def test_empty_inputs(shape, causal):
+    """No launch: an empty batch or no query rows give empty outputs; rows that see no key give
+    O = 0 and LSE = -inf (the reference's l = 0 with its 1e-9 term); every gradient is zero."""
+    B, Hq, Hkv, Sq, Skv = shape
+    D = 64
+    q = torch.randn(B, Hq, Sq, D, device=DEV, dtype=torch.float16, requires_grad=True)
+    k = torch.randn(B, Hkv, Skv, D, device=DEV, dtype=torch.float16, requires_grad=True)
+    v = torch.randn(B, Hkv, Skv, D, device=DEV, dtype=torch.float16, requires_grad=True)
+    o = co_alibi_attention(q, k, v, causal=causal)
+    assert o.shape == (B, Hq, Sq, D) and o.dtype == torch.float16
+    assert torch.all(o == 0)
+    o.backward(torch.randn_like(o))
+    for t in (q, k, v):
+        assert t.grad is not None and t.grad.shape == t.shape and torch.all(t.grad == 0)
+    slopes = (2.0 * _get_coalibi_slopes(Hq)).to(DEV, torch.float16)
+    _, lse, _ = torch.ops.co_alibi.fwd(q.detach(), k.detach(), v.detach(), slopes, causal, 0.125, True)
+    assert lse.shape == (B, Hq, Sq) and torch.all(torch.isneginf(lse))
 
 
 # --------------------------------------------------------------------------- full-size configs
