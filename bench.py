@@ -212,7 +212,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the Co-ALiBi op is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+              "(each (batch, kv-head) unit runs on one GPU; the op needs no collective)", file=sys.stderr)
         sys.exit(2)
 
     if args.workload == "gpt":
