@@ -394,3 +394,38 @@ def test_random_shapes(case):
     got = hip_fwd_bwd(q, k, v, do, causal=causal)
     o, lse, dq, dk, dv = oracle_fwd_bwd(q, k, v, do, causal=causal)
     assert_parity(got, (o, dq, dk, dv), TOL[dtype], f"{case}", dtype, relative=True)
+
+
+def _wide_cases():
+    """A wider seeded sweep: COALIBI_WIDE_CASES cases (8 by default) from seed
+    COALIBI_WIDE_SEED.  Head dims up to 256, lengths up to 2100, up to 5 kv heads with up
+    to 8 query heads each, batch up to 3."""
+    import os
+
+    n = int(os.environ.get("COALIBI_WIDE_CASES", "8"))
+    g = torch.Generator().manual_seed(int(os.environ.get("COALIBI_WIDE_SEED", "4242")))
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=g))]  # noqa: E731
+    cases = []
+    for i in range(n):
+        D = pick([32, 64, 128, 256])
+        dtype = pick([torch.float16, torch.bfloat16] + ([torch.float32] if D != 256 else []))
+        Hkv = pick([1, 2, 3, 5])
+        grp = pick([1, 2, 3, 4, 8])
+        Sq = int(torch.randint(1, 2100, (1,), generator=g))
+        Skv = Sq if i % 3 else int(torch.randint(1, 2100, (1,), generator=g))
+        causal = bool(i % 4 != 3)
+        B = pick([1, 2, 3])
+        cases.append((B, Hkv * grp, Hkv, Sq, Skv, D, causal, dtype, i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _wide_cases(),
+                         ids=lambda c: "{}-B{}H{}/{}S{}x{}D{}{}-{}".format(c[8], *c[:6], "c" if c[6] else "n",
+                                                                        str(c[7])[6:]))
+def test_random_shapes_wide(case):
+    B, Hq, Hkv, Sq, Skv, D, causal, dtype, i = case
+    print(f"case {case}", flush=True)
+    q, k, v, do = rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=Sq * 13 + Skv + i)
+    got = hip_fwd_bwd(q, k, v, do, causal=causal)
+    o, lse, dq, dk, dv = oracle_fwd_bwd(q, k, v, do, causal=causal)
+    assert_parity(got, (o, dq, dk, dv), TOL[dtype], f"{case}", dtype, relative=True)
