@@ -179,3 +179,43 @@ def test_decode_lengths_are_clamped_to_the_bound():
     want = co_alibi_decode(q, k, v, seq_len=1000)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+def _random_decode_cases(n=10, seed=99):
+    """Seeded serving batches: 1-4 sequences of random lengths (0 included) over caches of
+    random capacity, 1-8 kv heads with 1-8 query heads each, every head dim and dtype."""
+    g = torch.Generator().manual_seed(seed)
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=g))]  # noqa: E731
+    cases = []
+    for i in range(n):
+        D = pick([32, 64, 128, 256])
+        dtype = pick([torch.float16, torch.bfloat16] + ([torch.float32] if D != 256 else []))
+        Hkv = pick([1, 2, 3, 8])
+        grp = pick([1, 2, 4, 5, 8])
+        B = pick([1, 2, 3, 4])
+        cap = int(torch.randint(1, 5000, (1,), generator=g))
+        lens = [int(torch.randint(0, cap + 1, (1,), generator=g)) for _ in range(B)]
+        cases.append((B, Hkv * grp, Hkv, cap, D, dtype, tuple(lens), i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_decode_cases(),
+                         ids=lambda c: "{}-B{}_Hq{}_Hkv{}_cap{}_D{}-{}".format(c[7], *c[:5], str(c[5])[6:]))
+def test_decode_random_batches(case):
+    B, Hq, Hkv, cap, D, dtype, lens, i = case
+    print(f"case {case}", flush=True)
+    q, k, v = cache_inputs(B, Hq, Hkv, cap, cap, D, dtype, seed=100 + i)
+    for b, n in enumerate(lens):
+        k[b, :, n:] = 100.0
+        v[b, :, n:] = -1000.0
+    seq = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    o, lse = co_alibi_decode(q.to(DEV), k.to(DEV), v.to(DEV), seq_len=seq, return_lse=True)
+    torch.cuda.synchronize()
+    for b, n in enumerate(lens):
+        if n == 0:
+            assert torch.equal(o[b].float().cpu(), torch.zeros(Hq, 1, D)), "empty sequence: O must be 0"
+            assert torch.isneginf(lse[b]).all(), "empty sequence: LSE must be -inf"
+            continue
+        ro, rlse = oracle_decode(q[b:b + 1], k[b:b + 1], v[b:b + 1], n)
+        check(f"o[{b}] (len {n})", o[b:b + 1], ro, TOL[dtype])
+        check(f"lse[{b}] (len {n})", lse[b:b + 1], rlse, TOL[dtype])
