@@ -24,7 +24,7 @@ def build(verbose: bool = False) -> None:
     oracle_build.build(verbose)
     # Host code only: ROCm's clang++ (for _Float16 on the host) with the HIP runtime headers,
     # no device pass.
-    rocm = os.path.dirname(os.path.dirname(_hipcc()))
+    rocm = os.environ.get("ROCM_PATH") or os.path.dirname(os.path.dirname(os.path.realpath(_hipcc())))
     cmd = [os.path.join(rocm, "llvm", "bin", "clang++"), "-O2", "-std=c++17", "-Wall", "-Werror",
            "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(rocm, "include"), SRC, oracle_build.OBJ,
            "-L", LIB_DIR, "-lco_alibi", "-L", os.path.join(rocm, "lib"), "-lamdhip64",
