@@ -2,7 +2,8 @@
 
 The Python oracle is itself pinned (tests/test_oracle.py: closed forms, brute force,
 finite differences); the two restatements share no code, so agreement to fp64 rounding
-on random tiny shapes pins the C one.  The C oracle is what the torch-free C-ABI check
+on random tiny shapes pins the C one.  It must also reproduce the committed golden
+fixtures (tests/golden/*.npz).  The C oracle is what the torch-free C-ABI check
 program (tests/capi/capi_check.cpp) compares the library against.
 """
 import ctypes
@@ -85,3 +86,23 @@ def test_c_oracle_planted_mistake_is_caught(lib):
     np.testing.assert_allclose(dq, dq_w.numpy(), rtol=1e-10, atol=1e-12)
     assert np.abs(dq - dq_no_slope.numpy()).max() > 1e-3
 
+
+
+def test_c_oracle_reproduces_golden(lib):
+    """The C oracle against the committed golden fixtures (written from the float64 Python oracle)."""
+    from tests.test_golden import GOLDEN, load_golden
+
+    assert GOLDEN
+    for path in GOLDEN:
+        t, causal, sm_scale, _, _ = load_golden(path)
+        B, Hq, Sq, D = t["q"].shape
+        Hkv, Skv = t["k"].shape[1], t["k"].shape[2]
+        qn, kn, vn, don, ln = (t[n].double().numpy().copy() for n in ("q", "k", "v", "do", "slopes"))
+        o, lse = np.zeros_like(qn), np.zeros((B, Hq, Sq))
+        dq, dk, dv = np.zeros_like(qn), np.zeros_like(kn), np.zeros_like(vn)
+        dims = (B, Hq, Hkv, Sq, Skv, D, int(causal))
+        lib.co_alibi_ref_forward(*dims, sm_scale, _ptr(ln), _ptr(qn), _ptr(kn), _ptr(vn), _ptr(o), _ptr(lse))
+        lib.co_alibi_ref_backward(*dims, sm_scale, _ptr(ln), _ptr(qn), _ptr(kn), _ptr(vn), _ptr(don), _ptr(dq),
+                                  _ptr(dk), _ptr(dv))
+        for name, got in dict(o=o, lse=lse, dq=dq, dk=dk, dv=dv).items():
+            np.testing.assert_allclose(got, t[name].double().numpy(), rtol=0, atol=1e-5, err_msg=f"{path}: {name}")
