@@ -396,6 +396,31 @@ def test_random_shapes(case):
     assert_parity(got, (o, dq, dk, dv), TOL[dtype], f"{case}", dtype, relative=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_non_contiguous_inputs(dtype):
+    """Views in a model's (B, S, H, D) layout, transposed to (B, H, S, D), and sliced views give
+    the same O and gradients, bit for bit, as contiguous copies of the same values (the
+    wrapper makes them contiguous, as co_alibi_attn.py:137-148 does)."""
+    B, Hq, Hkv, S, D = 2, 8, 2, 200, 64
+    g = torch.Generator().manual_seed(17)
+    qb = (torch.randn(B, S, Hq, D, generator=g) * 0.5).to(dtype).to(DEV)
+    kb = (torch.randn(B, S + 3, Hkv, D, generator=g) * 0.5).to(dtype).to(DEV)
+    vb = (torch.randn(B, S, Hkv, 2 * D, generator=g) * 0.5).to(dtype).to(DEV)
+    do = torch.randn(B, Hq, S, D, generator=g).to(dtype).to(DEV)
+    views = [qb.transpose(1, 2), kb[:, 3:].transpose(1, 2), vb[..., D:].transpose(1, 2)]
+    assert not any(t.is_contiguous() for t in views)
+    leaves = [t.detach().requires_grad_() for t in views]
+    dense = [t.detach().contiguous().requires_grad_() for t in views]
+    o1 = co_alibi_attention(*leaves)
+    o1.backward(do)
+    o2 = co_alibi_attention(*dense)
+    o2.backward(do)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    for a, b in zip(leaves, dense):
+        assert torch.equal(a.grad, b.grad)
+
+
 def _wide_cases():
     """A wider seeded sweep: COALIBI_WIDE_CASES cases (8 by default) from seed
     COALIBI_WIDE_SEED.  Head dims up to 256, lengths up to 2100, up to 5 kv heads with up
