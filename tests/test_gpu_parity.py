@@ -421,6 +421,23 @@ def test_non_contiguous_inputs(dtype):
         assert torch.equal(a.grad, b.grad)
 
 
+def test_partial_gradients():
+    """Only some inputs require grad: those get the same gradients as in the full backward,
+    the others get none (autograd semantics of co_alibi_attn.py:72-135)."""
+    q, k, v, do = (t.to(DEV) for t in rand_inputs(1, 4, 2, 150, 150, 64, torch.float16, seed=5))
+    full = [t.clone().requires_grad_() for t in (q, k, v)]
+    co_alibi_attention(*full).backward(do)
+    for mask in ((True, False, False), (False, True, False), (False, False, True), (False, True, True)):
+        ins = [t.clone().requires_grad_(m) for t, m in zip((q, k, v), mask)]
+        co_alibi_attention(*ins).backward(do)
+        torch.cuda.synchronize()
+        for t, f, m in zip(ins, full, mask):
+            if m:
+                assert torch.equal(t.grad, f.grad), f"mask {mask}"
+            else:
+                assert t.grad is None, f"mask {mask}"
+
+
 def _wide_cases():
     """A wider seeded sweep: COALIBI_WIDE_CASES cases (8 by default) from seed
     COALIBI_WIDE_SEED.  Head dims up to 256, lengths up to 2100, up to 5 kv heads with up
