@@ -76,10 +76,15 @@ def cpu_baseline(w, budget_s: float):
     """
     import torch
 
+    from co_alibi_attn.profiling import attention_flops
     from co_alibi_attn.workloads import make_inputs
     from oracle import co_alibi_ref as ref
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    # Every core of this process's affinity, within the CPU share the host grants one GPU's jobs
+    # (OMP_NUM_THREADS, 16 on the MI355X boxes): the share, not the whole host, is this run's CPU.
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    cores = min(affinity, share) if share > 0 else affinity
     torch.set_num_threads(cores)
     q, k, v, do = (t.float() for t in make_inputs(w, seed=0))
     lam = ref.slopes(w.heads_q, w.bias_max, dtype=w.dtype).float()
@@ -96,12 +101,14 @@ def cpu_baseline(w, budget_s: float):
                 break
         if secs >= budget_s:
             break
-    fwd, bwd = ref.flops(1, len(done), w.seq, w.seq, w.head_dim, w.causal)
+    fwd, bwd = attention_flops(1, len(done), w.seq, w.seq, w.head_dim, w.causal)
+    host_cores = os.cpu_count()
     sample = (f"{w.name} workload, {len(done)} of {w.batch * w.heads_q} (batch, head) slices "
               f"(first: {done[0]}, last: {done[-1]}), fwd+bwd fp32, {secs:.1f} s on {cores} threads "
-              f"of {cpu_model_name()}")
+              f"(CPU share of one GPU: OMP_NUM_THREADS={share or 'unset'}; affinity {affinity} cores, host "
+              f"{host_cores}) of {cpu_model_name()}")
     return {"value": round((fwd + bwd) / secs / 1e12, 5), "unit": "TFLOPS", "cores": cores, "kind": "port",
-            "sample": sample, "seconds": round(secs, 3)}
+            "sample": sample, "seconds": round(secs, 3), "affinity_cores": affinity, "host_cores": host_cores, "cpu_model": cpu_model_name()}
 
 
 def cpu_config_timing():
@@ -222,8 +229,8 @@ def main():
     import torch
 
     from co_alibi_attn import co_alibi_attention
+    from co_alibi_attn.profiling import attention_flops
     from co_alibi_attn.workloads import WORKLOADS, make_inputs
-    from oracle.co_alibi_ref import flops
 
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
@@ -232,7 +239,7 @@ def main():
     q.requires_grad_(True)
     k.requires_grad_(True)
     v.requires_grad_(True)
-    fwd_flops, bwd_flops = flops(w.batch, w.heads_q, w.seq, w.seq, w.head_dim, w.causal)
+    fwd_flops, bwd_flops = attention_flops(w.batch, w.heads_q, w.seq, w.seq, w.head_dim, w.causal)
     print(f"[bench] workload {w.name}: B{w.batch} Hq{w.heads_q} Hkv{w.heads_kv} S{w.seq} D{w.head_dim} "
           f"{dtype_name} causal={w.causal}", file=sys.stderr, flush=True)
 
@@ -294,30 +301,45 @@ def main():
     probe_tflops, clock_ghz = mfma_probe(dev)
     print(f"[bench] MFMA probe: {probe_tflops:.0f} TFLOP/s, clock {clock_ghz:.3f} GHz", file=sys.stderr, flush=True)
 
-    sdpa_ms = None
-    if args.sdpa and w.heads_q == w.heads_kv:
+    sdpa_ms, sdpa_mode = None, None
+    if args.sdpa:
         # Plain causal attention at the same shape and dtype (torch SDPA on ROCm), fwd + bwd:
-        # the cost of Co-ALiBi relative to ordinary attention.
+        # the cost of Co-ALiBi relative to ordinary attention.  Grouped heads go in with
+        # enable_gqa; where that path is unavailable, K and V are expanded to the query heads
+        # outside the timed region (the gradients then stay per query head).
         import torch.nn.functional as F
 
-        qs, ks, vs = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        qs, ks_, vs = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        gqa = w.heads_q != w.heads_kv
 
-        def sdpa_step():
-            qs.grad = ks.grad = vs.grad = None
-            F.scaled_dot_product_attention(qs, ks, vs, is_causal=w.causal).backward(do)
+        def sdpa_step(kk, vv, **kw):
+            qs.grad = ks_.grad = vs.grad = None
+            F.scaled_dot_product_attention(qs, kk, vv, is_causal=w.causal, **kw).backward(do)
 
+        run = lambda: sdpa_step(ks_, vs)  # noqa: E731
+        sdpa_mode = "mha"
+        if gqa:
+            try:
+                sdpa_step(ks_, vs, enable_gqa=True)
+                run = lambda: sdpa_step(ks_, vs, enable_gqa=True)  # noqa: E731
+                sdpa_mode = "enable_gqa"
+            except RuntimeError:
+                g = w.heads_q // w.heads_kv
+                kx = ks_.detach().repeat_interleave(g, dim=1).requires_grad_(True)
+                vx = vs.detach().repeat_interleave(g, dim=1).requires_grad_(True)
+                run = lambda: sdpa_step(kx, vx)  # noqa: E731
+                sdpa_mode = "expanded kv"
         for _ in range(3):
-            sdpa_step()
+            run()
         torch.cuda.synchronize()
         start.record()
         for _ in range(args.steps):
-            sdpa_step()
+            run()
         end.record()
         torch.cuda.synchronize()
         sdpa_ms = start.elapsed_time(end) / args.steps
-        del qs, ks, vs
-        print(f"[bench] torch SDPA causal fwd+bwd: {sdpa_ms:.3f} ms/step", file=sys.stderr, flush=True)
-
+        del qs, ks_, vs
+        print(f"[bench] torch SDPA causal fwd+bwd ({sdpa_mode}): {sdpa_ms:.3f} ms/step", file=sys.stderr, flush=True)
 
     out = {
         "metric": "fwd and bwd TFLOPS (and % of MFMA peak) at B4 H16 S4096 D128 fp16 causal",
@@ -349,6 +371,7 @@ def main():
                          "bwd_frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / probe_tflops, 4),
                          "dominant_kernel_frac": round(achieved / probe_tflops, 4)},
         "sdpa_ms_per_step": None if sdpa_ms is None else round(sdpa_ms, 4),
+        "sdpa_mode": sdpa_mode,
         "coalibi_over_sdpa": None if sdpa_ms is None else round(ms_step / sdpa_ms, 3),
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),

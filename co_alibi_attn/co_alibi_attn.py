@@ -101,7 +101,8 @@ class CoALIBIAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do):
         q, k, v, o, lse, zb, slopes = ctx.saved_tensors
-        dq, dk, dv = ops.bwd(do, q, k, v, o, lse, zb, slopes, ctx.causal, ctx.sm_scale)
+        dq, dk, dv = ops.backward_for(ctx.needs_input_grad, do, q, k, v, o, lse, zb, slopes, ctx.causal,
+                                      ctx.sm_scale)
         return dq, dk, dv, None, None, None
 
 

@@ -1,4 +1,5 @@
-"""PyTorch operators over the native library: ``co_alibi::fwd``, ``co_alibi::bwd``, ``co_alibi::decode``.
+"""PyTorch operators over the native library: ``co_alibi::fwd``, ``co_alibi::bwd``, ``co_alibi::bwd_dq``,
+``co_alibi::decode``.
 
 Each operator is one ``torch.library.custom_op`` around one C-ABI launch
 (include/co_alibi.h), so that:
@@ -28,7 +29,7 @@ from torch import Tensor
 
 from . import _native
 
-__all__ = ["fwd", "bwd", "decode", "zb_numel"]
+__all__ = ["fwd", "bwd", "bwd_dq", "backward_for", "decode", "zb_numel"]
 
 
 def zb_numel(batch: int, heads_q: int, seq_q: int, seq_kv: int) -> int:
@@ -114,11 +115,22 @@ def _fwd_setup_context(ctx, inputs, output):
     ctx.mark_non_differentiable(lse, zb)
 
 
+def backward_for(needs_input_grad, do, q, k, v, o, lse, zb, slopes, causal, sm_scale):
+    """(dq, dk, dv) for the inputs whose flag in ``needs_input_grad`` (q, k, v first) is set,
+    None for the others.  dK needs backward pass 1's per-row statistics, so pass 1 runs
+    whenever any gradient is wanted; pass 2 runs only when dK or dV is."""
+    need_q, need_k, need_v = needs_input_grad[:3]
+    if not (need_k or need_v):
+        return (bwd_dq(do, q, k, v, o, lse, zb, slopes, causal, sm_scale) if need_q else None), None, None
+    dq, dk, dv = bwd(do, q, k, v, o, lse, zb, slopes, causal, sm_scale)
+    return dq if need_q else None, dk if need_k else None, dv if need_v else None
+
+
 def _fwd_backward(ctx, do, _dlse, _dzb):
     if not ctx.with_stats:
         raise RuntimeError("co_alibi::fwd ran with with_stats=False (inference) and has no backward")
     q, k, v, o, lse, zb, slopes = ctx.saved_tensors
-    dq, dk, dv = bwd(do, q, k, v, o, lse, zb, slopes, ctx.causal, ctx.sm_scale)
+    dq, dk, dv = backward_for(ctx.needs_input_grad, do, q, k, v, o, lse, zb, slopes, ctx.causal, ctx.sm_scale)
     return dq, dk, dv, None, None, None, None
 
 
@@ -162,6 +174,40 @@ def _bwd_fake(do, q, k, v, o, lse, zb, slopes, causal, sm_scale):
     cf = torch.contiguous_format
     return (torch.empty_like(q, memory_format=cf), torch.empty_like(k, memory_format=cf),
             torch.empty_like(v, memory_format=cf))
+
+
+@torch.library.custom_op("co_alibi::bwd_dq", mutates_args=(), device_types="cuda")
+def bwd_dq(do: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor, zb: Tensor, slopes: Tensor,
+           causal: bool, sm_scale: float) -> Tensor:
+    """dQ alone (backward pass 1, the C ABI's co_alibi_bwd_dq), for callers whose k and v need no
+    gradient: the same dq as co_alibi::bwd, bit for bit, without the key-major pass 2."""
+    batch, heads_q, seq_q, head_dim = q.shape
+    heads_kv, seq_kv = k.shape[1], k.shape[2]
+    if q.numel() == 0 or k.numel() == 0:
+        return torch.zeros(q.shape, device=q.device, dtype=q.dtype)
+    q, k, v, o = _aligned(q), _aligned(k), _aligned(v), _aligned(o)
+    do = _aligned(do.to(q.dtype))
+    lse, zb = lse.contiguous(), zb.contiguous()
+    slopes32 = slopes.detach().to(device=q.device, dtype=torch.float32).contiguous()
+    dq = torch.empty_like(q)
+    lib = _native.lib()
+    ws_bytes = lib.co_alibi_bwd_workspace_bytes(batch, heads_q, seq_q, seq_kv)
+    workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        _native.check(
+            lib.co_alibi_bwd_dq(
+                _native.DTYPE_CODES[q.dtype], do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                o.data_ptr(), lse.data_ptr(), zb.data_ptr(), slopes32.data_ptr(), dq.data_ptr(),
+                workspace.data_ptr(), ws_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim,
+                1 if causal else 0, float(sm_scale), _stream(q.device),
+            )
+        )
+    return dq
+
+
+@bwd_dq.register_fake
+def _bwd_dq_fake(do, q, k, v, o, lse, zb, slopes, causal, sm_scale):
+    return torch.empty_like(q, memory_format=torch.contiguous_format)
 
 
 # ----------------------------------------------------------------------------- decode

@@ -58,6 +58,16 @@ MI355X_XCDS = 8    # GRBM_GUI_ACTIVE is read once per XCD
 PRODUCTS = {"coalibi_fwd_kernel": (2, 2), "coalibi_bwd_dq_kernel": (1, 3), "coalibi_bwd_dkdv_kernel": (4, 4)}
 
 
+def attention_flops(batch, heads_q, seq_q, seq_kv, head_dim, causal=True):
+    """Algorithmic (forward, backward) flops of one attention call in the FlashAttention convention:
+    forward 2 products of 2*B*Hq*D flops per (query, key) pair, over Sq*Skv pairs halved when
+    causal, and backward 2.5 times the forward.  The reference's harness counts the full square
+    with backward 2x (co_alibi_attn/benchmark_flops.py:139-140), 2x / 1.6x these figures."""
+    pairs = seq_q * seq_kv / 2.0 if causal else float(seq_q * seq_kv)
+    fwd = 4.0 * batch * heads_q * head_dim * pairs
+    return fwd, 2.5 * fwd
+
+
 class KernelSet:
     """Device buffers of one workload and a launcher per kernel, all through the C ABI on one stream."""
 
@@ -105,8 +115,7 @@ class KernelSet:
 
         self.launch = dict(zip(KERNELS, (fwd, dq, dkdv)))
         self.launch["coalibi_fwd_kernel (inference)"] = fwd_inference
-        pairs = S * S / 2.0 if w.causal else float(S * S)
-        self.gemm_flops = 2.0 * B * Hq * D * pairs
+        self.gemm_flops = attention_flops(B, Hq, S, S, D, w.causal)[0] / 2.0  # one product
 
     def charged_flops(self, name: str) -> float:
         return PRODUCTS[name][0] * self.gemm_flops

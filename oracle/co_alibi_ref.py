@@ -169,11 +169,3 @@ def forward_autograd(q, k, v, lam, causal=True, scale=None):
     e = torch.exp(a - m).masked_fill(mask, 0.0)
     s = e / (e.sum(dim=-1, keepdim=True) + 1e-9)
     return torch.einsum("bhij,bhjd->bhid", s, v)
-
-
-def flops(batch, heads_q, seq_q, seq_kv, head_dim, causal=True):
-    """Algorithmic flops, FlashAttention convention: fwd 4*B*H*Sq*Skv*D (halved when causal), bwd 2.5x."""
-    fwd = 4.0 * batch * heads_q * seq_q * seq_kv * head_dim
-    if causal:
-        fwd /= 2.0
-    return fwd, 2.5 * fwd

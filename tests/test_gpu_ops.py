@@ -43,6 +43,9 @@ def test_opcheck_fwd_bwd(dtype):
                           test_utils=("test_schema", "test_autograd_registration", "test_faketensor"))
     o, lse, zb = torch.ops.co_alibi.fwd(q, k, v, sl, True, scale, True)
     torch.library.opcheck(torch.ops.co_alibi.bwd, (do, q, k, v, o, lse, zb, sl, True, scale))
+    torch.library.opcheck(torch.ops.co_alibi.bwd_dq, (do, q, k, v, o, lse, zb, sl, True, scale))
+    dq_full = torch.ops.co_alibi.bwd(do, q, k, v, o, lse, zb, sl, True, scale)[0]
+    assert torch.equal(torch.ops.co_alibi.bwd_dq(do, q, k, v, o, lse, zb, sl, True, scale), dq_full)
 
 
 def test_opcheck_decode():

@@ -3,15 +3,17 @@
 Bar: max-abs <= 1e-4 in the fp32 validation mode,
 <= 2e-2 for O, dQ, dK, dV with fp16/bf16 inputs, against the oracle run in
 fp32 on the same (dtype-rounded) inputs with the same dtype-rounded slopes.
-Outputs are returned in the input dtype, whose own rounding is half an ulp of
-the value (2^-8 relative in bf16, 2^-11 in fp16): where a 16-bit output is large
-(grouped-query dK/dV sums reach 8-16, where half a bf16 ulp is 0.031) the bar is
-applied to the error beyond that rounding, |got - ref| - half_ulp * |ref|.  The
-seeded random-shape sweep (outputs up to ~40 from sums over many rows and grouped
-heads, where 16-bit products bound the error relative to the magnitude) divides
-the error by max(1, max |ref|).
-Every GPU call goes through the C ABI (directly, or via the drop-in API which
-is a thin ctypes layer over it).
+
+The bar is applied as written, with no allowance, to every output whose largest
+reference value is at most REF_SCALE[dtype].  Past that magnitude no kernel can
+meet an absolute bar: the output type's own rounding is up to half an ulp of the
+value, |x| 2^-9 in bf16 (already 2e-2 at |x| = 5.1) and |x| 2^-12 in fp16, and
+sums over many rows and grouped heads carry error relative to their size.  Such
+outputs (grouped-query dK/dV, non-causal sums, reaching 10-160 in the random
+sweeps) get the bar scaled by max|ref| / REF_SCALE[dtype]; the worst error as a
+share of its bar is printed per dtype at the end of the module.
+Every GPU call goes through the C ABI (directly, or via the drop-in API and the
+torch operators over it).
 """
 import ctypes
 import math
@@ -20,7 +22,7 @@ import pytest
 import torch
 
 from co_alibi_attn import _native, co_alibi_attention
-from co_alibi_attn.co_alibi_attn import _get_coalibi_slopes
+from co_alibi_attn.co_alibi_attn import CoALIBIAttention, _get_coalibi_slopes
 from co_alibi_attn.workloads import WORKLOADS, make_inputs
 from oracle import co_alibi_ref as ref
 from tests.test_golden import GOLDEN, load_golden
@@ -57,27 +59,32 @@ def rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=0, scale=0.5):
     return q, k, v, do
 
 
-HALF_ULP = {torch.float32: 0.0, torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}
+# Largest reference magnitude at which the absolute bar applies unchanged (see the module docstring).
+REF_SCALE = {torch.float32: 4.0, torch.float16: 16.0, torch.bfloat16: 4.0}
+WORST = {}  # dtype name -> (worst error / bar, label)
 
 
-def assert_parity(got, want, tol, label, dtype=torch.float32, relative=False):
-    """max-abs <= tol, counting only the error beyond the output dtype's own rounding.
-
-    relative=True divides the error by max(1, max |ref|) of the output: the bar for
-    shapes whose outputs grow large (sums over many rows and heads), where 16-bit
-    products bound the error relative to the magnitude; indexing mistakes still show
-    as errors of the order of the output.
-    """
+def assert_parity(got, want, tol, label, dtype=torch.float32):
+    """max-abs <= tol for outputs up to REF_SCALE[dtype] in magnitude, tol * max|ref| / REF_SCALE beyond."""
     for name, g, w in zip(("o", "dq", "dk", "dv"), got, want):
         assert torch.isfinite(g).all(), f"{label}: {name} has non-finite values"
         w = w.float()
-        diff = (g - w).abs()
-        err = diff.max().item()
-        excess = (diff - HALF_ULP[dtype] * w.abs()).max().item()
-        scale = max(1.0, w.abs().max().item()) if relative else 1.0
-        print(f"  {label} {name}: max-abs {err:.3e}, beyond output rounding {excess:.3e}, |ref| max {scale:.2f} "
-              f"(tol {tol:g}{' x |ref|' if relative else ''})", flush=True)
-        assert excess <= tol * scale, f"{label}: {name} max-abs {err:.3e} ({excess:.3e} beyond output rounding) > {tol * scale:g}"
+        err = (g - w).abs().max().item()
+        ref_max = w.abs().max().item()
+        bar = tol * max(1.0, ref_max / REF_SCALE[dtype])
+        key = str(dtype).split(".")[-1]
+        if err / bar > WORST.get(key, (0.0, ""))[0]:
+            WORST[key] = (err / bar, f"{label} {name}")
+        print(f"  {label} {name}: max-abs {err:.3e}, |ref| max {ref_max:.2f}, bar {bar:.3g} "
+              f"({err / bar:.0%} of it)", flush=True)
+        assert err <= bar, f"{label}: {name} max-abs {err:.3e} > {bar:.3g}"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _report_worst_ratio():
+    yield
+    for key, (ratio, label) in sorted(WORST.items()):
+        print(f"worst error / bar, {key}: {ratio:.1%} ({label})", flush=True)
 
 
 def hip_fwd_raw(q, k, v, slopes, causal, sm_scale):
@@ -293,46 +300,36 @@ def test_empty_inputs(shape, causal):
 
 # --------------------------------------------------------------------------- full-size configs
 
-# Sampled (batch, query head) pairs checked against the oracle; dK/dV of a key
-# head are checked only where all its query heads are sampled.
-FULL = {
-    "headline": [(0, 0), (3, 15)],
-    "gqa": [(0, 4), (0, 5), (0, 6), (0, 7)],
-    "long": [(0, 0), (0, 7)],
-}
+FULL = ("headline", "gqa", "long")
 
 
-@pytest.mark.parametrize("name", list(FULL))
+@pytest.mark.parametrize("name", FULL)
 def test_full_size_config(name):
+    """BASELINE configs[1..3] at full size: every (batch, query head) of O and dQ and every
+    (batch, key head) of dK and dV against the chunked CPU oracle, with the bar of assert_parity."""
     w = WORKLOADS[name]
     print(f"config {name}: B{w.batch} Hq{w.heads_q} Hkv{w.heads_kv} S{w.seq} D{w.head_dim} {w.dtype}", flush=True)
     q, k, v, do = make_inputs(w, seed=0)
-    o, dq, dk, dv = hip_fwd_bwd(q, k, v, do, causal=w.causal, bias_max=w.bias_max)
-    for name_, t in dict(o=o, dq=dq, dk=dk, dv=dv).items():
-        assert torch.isfinite(t).all(), f"{name_} not finite"
+    got = hip_fwd_bwd(q, k, v, do, causal=w.causal, bias_max=w.bias_max)
     # Size-independent identity: sum over keys of dV = sum over rows of dO (weights sum to 1).
     g = w.heads_q // w.heads_kv
+    dv = got[3]
     dv_sum = dv.double().sum(2)                                             # (B, Hkv, D)
     do_sum = do.double().view(w.batch, w.heads_kv, g, w.seq, w.head_dim).sum((2, 3))
     rel = ((dv_sum - do_sum).abs().max() / do_sum.abs().max()).item()
     print(f"  sum_j dV_j vs sum_i dO_i: rel {rel:.2e}", flush=True)
     assert rel < 1e-2
-    heads = FULL[name]
-    ro, _, rdq, rdk, rdv = oracle_fwd_bwd(q, k, v, do, causal=w.causal, bias_max=w.bias_max, heads=heads)
-    for b, h in heads:
-        for n_, got, want in (("o", o, ro), ("dq", dq, rdq)):
-            err = (got[b, h] - want[b, h]).abs().max().item()
-            print(f"  {name} b{b} h{h} {n_}: max-abs {err:.3e}", flush=True)
-            assert err <= TOL[w.dtype]
-    kv_heads = {(b, h // g) for b, h in heads if all((b, hh) in heads for hh in range((h // g) * g, (h // g + 1) * g))}
-    for b, hk in sorted(kv_heads):
-        for n_, got, want in (("dk", dk, rdk), ("dv", dv, rdv)):
-            err = (got[b, hk] - want[b, hk]).abs().max().item()
-            print(f"  {name} b{b} kv{hk} {n_}: max-abs {err:.3e}", flush=True)
-            assert err <= TOL[w.dtype]
+    ro, _, rdq, rdk, rdv = oracle_fwd_bwd(q, k, v, do, causal=w.causal, bias_max=w.bias_max)
+    # Per-head maxima, so a failure names its head.
+    for n_, a_, b_ in zip(("o", "dq", "dk", "dv"), got, (ro, rdq, rdk, rdv)):
+        per_head = (a_ - b_).abs().amax(dim=(2, 3))
+        b0, h0 = divmod(int(per_head.argmax()), per_head.shape[1])
+        print(f"  {name} {n_}: worst head (b{b0}, h{h0}) max-abs {per_head.max().item():.3e} over "
+              f"{per_head.numel()} heads", flush=True)
+    assert_parity(got, (ro, rdq, rdk, rdv), TOL[w.dtype], f"{name} (all heads)", w.dtype)
 
 
-@pytest.mark.parametrize("name", list(FULL))
+@pytest.mark.parametrize("name", FULL)
 def test_full_size_invariances(name):
     """Identities of the math at the BASELINE sizes, over every head (the oracle above samples a few):
     - the backward is linear in dO: doubling dO doubles dQ, dK and dV (x2 is exact; the 16-bit
@@ -393,7 +390,7 @@ def test_random_shapes(case):
     q, k, v, do = rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=Sq * 7 + Skv)
     got = hip_fwd_bwd(q, k, v, do, causal=causal)
     o, lse, dq, dk, dv = oracle_fwd_bwd(q, k, v, do, causal=causal)
-    assert_parity(got, (o, dq, dk, dv), TOL[dtype], f"{case}", dtype, relative=True)
+    assert_parity(got, (o, dq, dk, dv), TOL[dtype], f"{case}", dtype)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
@@ -470,4 +467,42 @@ def test_random_shapes_wide(case):
     q, k, v, do = rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=Sq * 13 + Skv + i)
     got = hip_fwd_bwd(q, k, v, do, causal=causal)
     o, lse, dq, dk, dv = oracle_fwd_bwd(q, k, v, do, causal=causal)
-    assert_parity(got, (o, dq, dk, dv), TOL[dtype], f"{case}", dtype, relative=True)
+    assert_parity(got, (o, dq, dk, dv), TOL[dtype], f"{case}", dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
+@pytest.mark.parametrize("kv_form", ["expanded", "grouped", "mha"])
+def test_autograd_function_apply(kv_form, dtype):
+    """The reference's autograd function, CoALIBIAttention.apply(q, k, v, slopes, causal, sm_scale)
+    (co_alibi_attn.py:24-135), forward and backward on the GPU against the oracle.
+
+    expanded: K / V of 2 key heads repeated to the 8 query heads with repeat_interleave inside
+      autograd, exactly as the reference's wrapper passes them (co_alibi_attn.py:143-147); the
+      gradients of the unexpanded K / V are the group sums autograd forms through the repeat;
+    grouped: the same K / V passed with their 2 heads (the native grouped-query form);
+    mha: 8 key heads of their own.
+    """
+    B, Hq, S, D = 2, 8, 200, 64
+    Hkv = 8 if kv_form == "mha" else 2
+    print(f"apply {kv_form} {dtype}", flush=True)
+    q, k, v, do = rand_inputs(B, Hq, Hkv, S, S, D, dtype, seed=11)
+    slopes = (2.0 * _get_coalibi_slopes(Hq, 8.0)).to(DEV, dtype)  # co_alibi_attn.py:147
+    sm_scale = 1.0 / math.sqrt(D)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    if kv_form == "expanded":
+        g = Hq // Hkv
+        ka, va = kd.repeat_interleave(g, dim=1), vd.repeat_interleave(g, dim=1)
+    else:
+        ka, va = kd, vd
+    o = CoALIBIAttention.apply(qd, ka, va, slopes, True, sm_scale)
+    assert o.shape == (B, Hq, S, D) and o.dtype == dtype and o.grad_fn is not None
+    o.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    got = tuple(t.detach().float().cpu() for t in (o, qd.grad, kd.grad, vd.grad))
+    ro, _, rdq, rdk, rdv = oracle_fwd_bwd(q, k, v, do, causal=True)
+    assert_parity(got, (ro, rdq, rdk, rdv), TOL[dtype], f"apply {kv_form}", dtype)
+    # The drop-in entry point (native grouped heads, no expansion) gives the same values.
+    ref_api = hip_fwd_bwd(q, k, v, do, causal=True)
+    tol = 0.0 if kv_form != "expanded" else TOL[dtype]
+    for name, a, b in zip(("o", "dq", "dk", "dv"), got, ref_api):
+        assert (a - b).abs().max().item() <= tol, f"apply {kv_form}: {name} differs from co_alibi_attention"

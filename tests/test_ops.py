@@ -17,6 +17,9 @@ def test_operators_are_registered_with_their_schemas():
     fwd = str(torch.ops.co_alibi.fwd.default._schema)
     bwd = str(torch.ops.co_alibi.bwd.default._schema)
     dec = str(torch.ops.co_alibi.decode.default._schema)
+    bwd_dq = str(torch.ops.co_alibi.bwd_dq.default._schema)
+    assert bwd_dq == ("co_alibi::bwd_dq(Tensor do, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor zb, "
+                      "Tensor slopes, bool causal, float sm_scale) -> Tensor")
     assert fwd == ("co_alibi::fwd(Tensor q, Tensor k, Tensor v, Tensor slopes, bool causal, float sm_scale, "
                    "bool with_stats) -> (Tensor, Tensor, Tensor)")
     assert bwd == ("co_alibi::bwd(Tensor do, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor zb, "
@@ -55,6 +58,23 @@ def test_fwd_autograd_reaches_bwd():
     o.float().sum().backward()
     for t in (q, k, v):
         assert t.grad.shape == t.shape and t.grad.dtype == t.dtype
+
+
+@pytest.mark.parametrize("mask", [(True, False, False), (False, True, False), (False, False, True), (True, True, False)])
+def test_partial_gradients_reach_the_right_operator(mask, monkeypatch):
+    """Only the inputs that require grad get one; dQ alone runs co_alibi::bwd_dq (pass 1 only),
+    any key / value gradient runs co_alibi::bwd."""
+    B, Hq, Hkv, S, D = 1, 4, 2, 64, 64
+    called = []
+    for name in ("bwd", "bwd_dq"):
+        op = getattr(ops, name)
+        monkeypatch.setattr(ops, name, lambda *a, _op=op, _n=name: called.append(_n) or _op(*a))
+    q, k, v = (meta(B, h, S, D, grad=m) for h, m in zip((Hq, Hkv, Hkv), mask))
+    o, _, _ = torch.ops.co_alibi.fwd(q, k, v, meta(Hq), True, 0.125, True)
+    o.float().sum().backward()
+    assert called == (["bwd_dq"] if mask == (True, False, False) else ["bwd"])
+    for t, m in zip((q, k, v), mask):
+        assert (t.grad is not None) == m
 
 
 def test_inference_forward_has_no_backward():

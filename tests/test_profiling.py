@@ -58,3 +58,20 @@ def test_counter_normalisation(tmp_path):
     cells = [c.strip() for c in row.split("|")[1:-1]]
     # MFMA busy, VALU busy, VALU/MFMA, trans/MFMA, LDS/MFMA, conflict per LDS instr, conflict share, GB/s
     assert cells[1:] == ["25.0 %", "50.0 %", "12.00", "3.00", "0.50", "1.600", "20.0 %", "2000"]
+
+
+def test_attention_flops_closed_form():
+    """FlashAttention convention: fwd 4*B*Hq*Sq*Skv*D, halved when causal, bwd 2.5x.  At the
+    headline shape that is 2.749e11 / 6.872e11 flops; the reference's own harness counts the
+    full square with bwd 2x (benchmark_flops.py:139-140), i.e. 2x the causal forward here."""
+    from co_alibi_attn.profiling import attention_flops
+
+    fwd, bwd = attention_flops(4, 16, 4096, 4096, 128, causal=True)
+    assert fwd == 4 * 4 * 16 * 4096 * 4096 * 128 / 2 and round(fwd / 1e11, 3) == 2.749
+    assert bwd == 2.5 * fwd and round(bwd / 1e11, 3) == 6.872
+    ref_fwd = 4 * 4 * 16 * 4096 * 4096 * 128  # benchmark_flops.py:139
+    assert ref_fwd == 2 * fwd
+    nc_fwd, nc_bwd = attention_flops(1, 2, 100, 300, 64, causal=False)
+    assert nc_fwd == 4 * 2 * 100 * 300 * 64 and nc_bwd == 2.5 * nc_fwd
+    # one product of the per-kernel accounting is half the forward
+    assert attention_flops(1, 1, 8, 8, 32, causal=True)[0] == 2 * (2 * 32 * 8 * 8 / 2)
