@@ -16,6 +16,9 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 SUPPORTED_HEAD_DIMS = (32, 64, 128, 256)
 
+# Size of the library-held split-K scratch of co_alibi_decode_noalloc (CO_ALIBI_DECODE_SCRATCH_BYTES).
+DECODE_SCRATCH_BYTES = 32 << 20
+
 # Symbols declared in include/co_alibi.h.
 EXPORTS = (
     "co_alibi_zb_numel",
@@ -26,6 +29,7 @@ EXPORTS = (
     "co_alibi_bwd_dkdv",
     "co_alibi_decode_workspace_bytes",
     "co_alibi_decode",
+    "co_alibi_decode_noalloc",
     "co_alibi_probe_mfma",
     "co_alibi_last_error",
     "co_alibi_abi_version",
@@ -54,6 +58,7 @@ _SIGNATURES = {
     ),
     "co_alibi_decode_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "co_alibi_decode": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "co_alibi_decode_noalloc": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
     "co_alibi_probe_mfma": (_I, [_P, _P, _I, _I, _P]),
     "co_alibi_last_error": (ctypes.c_char_p, []),
     "co_alibi_abi_version": (_I, []),

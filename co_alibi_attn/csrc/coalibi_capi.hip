@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/co_alibi.h"
@@ -280,21 +281,62 @@ int device_cus() {
   return n;
 }
 
-}  // namespace
+// Split count of a decode launch: enough splits to give every CU kDecodeWGsPerCU work-groups
+// (each split walks cps consecutive 128-key chunks), at most decode_splits_max.
+struct DecodeSplit {
+  int nChunks, cps, nSplits;
+};
+DecodeSplit decode_split(int batch, int heads_kv, int seq_kv) {
+  DecodeSplit d{};
+  d.nChunks = static_cast<int>(decode_chunks(seq_kv));
+  const long long units = static_cast<long long>(batch) * heads_kv;
+  const long long want = (static_cast<long long>(coalibi::kDecodeWGsPerCU) * device_cus() + units - 1) / units;
+  const int splits = static_cast<int>(std::max(1LL, std::min<long long>(want, decode_splits_max(seq_kv))));
+  d.cps = (d.nChunks + splits - 1) / splits;
+  d.nSplits = (d.nChunks + d.cps - 1) / d.cps;
+  return d;
+}
 
-extern "C" {
-
-size_t co_alibi_decode_workspace_bytes(int batch, int heads_q, int seq_kv, int head_dim) {
-  if (batch < 1 || heads_q < 1 || seq_kv < 1 || head_dim < 1) return 0;
-  const size_t parts = static_cast<size_t>(batch) * heads_q * decode_splits_max(seq_kv);
+// Bytes of split-K partials for `parts` (batch, query head, split) triples: the maximum, the sum
+// and the sigma total (one 256-byte aligned fp32 array each), then head_dim floats of O per part.
+size_t decode_partials_bytes(size_t parts, int head_dim) {
   return 3 * round_up(parts * sizeof(float), 256) + parts * head_dim * sizeof(float);
 }
 
-int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v_cache, const float* slopes,
-                    const int* seq_lens, void* o, float* lse, void* workspace, size_t workspace_bytes, int batch,
-                    int heads_q, int heads_kv, int seq_kv, int kv_capacity, int head_dim, float sm_scale,
-                    void* stream) {
-  const char* fn = "co_alibi_decode";
+// Device scratch of co_alibi_decode_noalloc: the split-K partials of callers that cannot
+// allocate.  Each GPU holds its own copy for the life of the process.  Host code never uses
+// this name as an address: its device address, per device, comes from hipGetSymbolAddress.
+constexpr size_t kDecodeScratchBytes = CO_ALIBI_DECODE_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+// The device address of `scratch` on the current device, looked up once per device (with that
+// device current) and kept.
+int scratch_address(const char* fn, void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(CO_ALIBI_ELAUNCH, std::string(fn) + ": no current HIP device");
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(CO_ALIBI_ELAUNCH, std::string(fn) + ": scratch lookup failed: " + hipGetErrorString(e));
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return CO_ALIBI_OK;
+}
+
+// co_alibi_decode and co_alibi_decode_noalloc.  The caller's workspace is laid out for the
+// largest split count a decode of seq_kv keys can take (its size depends on the shape only);
+// the library's scratch is laid out for this launch's split count, which fits more.
+int decode_impl(const char* fn, bool scratch_ws, int dtype, const void* q, const void* k_cache,
+                const void* v_cache, const float* slopes, const int* seq_lens, void* o, float* lse,
+                void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv, int seq_kv,
+                int kv_capacity, int head_dim, float sm_scale, void* stream) {
   const Shape s{batch, heads_q, heads_kv, 1, seq_kv, head_dim};
   int rc;
   if ((rc = check_shape(fn, dtype, s))) return rc;
@@ -310,13 +352,21 @@ int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v
       (rc = check_ptr(fn, "slopes", slopes, 4)) || (rc = check_opt_ptr(fn, "seq_lens", seq_lens, 4)) ||
       (rc = check_opt_ptr(fn, "lse", lse, 4)) || (rc = check_ptr(fn, "workspace", workspace, 256)))
     return rc;
-  const size_t need = co_alibi_decode_workspace_bytes(batch, heads_q, seq_kv, head_dim);
-  if (workspace_bytes < need)
-    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": workspace of " + std::to_string(workspace_bytes) +
-                                     " bytes, need " + std::to_string(need));
   if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": sm_scale must be finite");
 
-  const size_t parts = static_cast<size_t>(batch) * heads_q * decode_splits_max(seq_kv);
+  const DecodeSplit sp = decode_split(batch, heads_kv, seq_kv);
+  const size_t rows = static_cast<size_t>(batch) * heads_q;
+  const size_t parts = rows * (scratch_ws ? static_cast<size_t>(sp.nSplits) : decode_splits_max(seq_kv));
+  const size_t need = decode_partials_bytes(parts, head_dim);
+  if (workspace_bytes < need) {
+    if (scratch_ws)
+      return fail(CO_ALIBI_EINVAL, std::string(fn) + ": the split-K partials of this decode need " +
+                                       std::to_string(need) + " bytes, above the library scratch of " +
+                                       std::to_string(workspace_bytes) + " bytes");
+    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": workspace of " + std::to_string(workspace_bytes) +
+                                     " bytes, need " + std::to_string(need));
+  }
+
   const size_t stat_bytes = round_up(parts * sizeof(float), 256);
   char* ws = static_cast<char*>(workspace);
   coalibi::DecodeArgs a{};
@@ -337,13 +387,9 @@ int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v
   a.G = heads_q / heads_kv;
   a.L = seq_kv;
   a.cap = kv_capacity;
-  a.nChunks = static_cast<int>(decode_chunks(seq_kv));
-  // Enough splits to give every CU kDecodeWGsPerCU work-groups; each walks cps chunks.
-  const long long units = static_cast<long long>(batch) * heads_kv;
-  const long long want = (static_cast<long long>(coalibi::kDecodeWGsPerCU) * device_cus() + units - 1) / units;
-  const int splits = static_cast<int>(std::max(1LL, std::min<long long>(want, decode_splits_max(seq_kv))));
-  a.cps = (a.nChunks + splits - 1) / splits;
-  a.nSplits = (a.nChunks + a.cps - 1) / a.cps;
+  a.nChunks = sp.nChunks;
+  a.cps = sp.cps;
+  a.nSplits = sp.nSplits;
   a.sc2 = sm_scale * coalibi::kLog2eHost;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
@@ -354,6 +400,33 @@ int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v
   }
   if (e != hipSuccess) return fail(CO_ALIBI_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
   return CO_ALIBI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t co_alibi_decode_workspace_bytes(int batch, int heads_q, int seq_kv, int head_dim) {
+  if (batch < 1 || heads_q < 1 || seq_kv < 1 || head_dim < 1) return 0;
+  return decode_partials_bytes(static_cast<size_t>(batch) * heads_q * decode_splits_max(seq_kv), head_dim);
+}
+
+int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v_cache, const float* slopes,
+                    const int* seq_lens, void* o, float* lse, void* workspace, size_t workspace_bytes, int batch,
+                    int heads_q, int heads_kv, int seq_kv, int kv_capacity, int head_dim, float sm_scale,
+                    void* stream) {
+  return decode_impl("co_alibi_decode", false, dtype, q, k_cache, v_cache, slopes, seq_lens, o, lse, workspace,
+                     workspace_bytes, batch, heads_q, heads_kv, seq_kv, kv_capacity, head_dim, sm_scale, stream);
+}
+
+int co_alibi_decode_noalloc(int dtype, const void* q, const void* k_cache, const void* v_cache,
+                            const float* slopes, const int* seq_lens, void* o, float* lse, int batch, int heads_q,
+                            int heads_kv, int seq_kv, int kv_capacity, int head_dim, float sm_scale, void* stream) {
+  const char* fn = "co_alibi_decode_noalloc";
+  void* ws = nullptr;
+  if (const int rc = scratch_address(fn, &ws)) return rc;
+  return decode_impl(fn, true, dtype, q, k_cache, v_cache, slopes, seq_lens, o, lse, ws, kDecodeScratchBytes, batch,
+                     heads_q, heads_kv, seq_kv, kv_capacity, head_dim, sm_scale, stream);
 }
 
 const char* co_alibi_last_error(void) { return g_last_error.c_str(); }

@@ -111,6 +111,21 @@ int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v
                     void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv,
                     int seq_kv, int kv_capacity, int head_dim, float sm_scale, void* stream);
 
+/* co_alibi_decode for callers that cannot allocate device memory (work captured into a HIP
+ * graph, tight serving loops, harnesses that forbid hipMalloc).  It has no counterpart in the
+ * reference.  Arguments are those of co_alibi_decode without the workspace: the split-K
+ * partials go to a buffer of CO_ALIBI_DECODE_SCRATCH_BYTES that the library holds on every GPU
+ * it runs on until the process ends, laid out for this launch's split count ((4 + head_dim)
+ * fp32 per (batch, query head, split), each of the three per-split arrays 256-byte aligned).  A
+ * decode whose partials exceed it returns CO_ALIBI_EINVAL.  The call allocates nothing.  All
+ * calls on one GPU share its buffer, which keeps the last call's contents: calls that overlap on
+ * one GPU (for instance on two streams) race, so order them on one stream. */
+#define CO_ALIBI_DECODE_SCRATCH_BYTES (32u << 20)
+int co_alibi_decode_noalloc(int dtype, const void* q, const void* k_cache, const void* v_cache,
+                            const float* slopes, const int* seq_lens, void* o, float* lse, int batch,
+                            int heads_q, int heads_kv, int seq_kv, int kv_capacity, int head_dim,
+                            float sm_scale, void* stream);
+
 /* Measurement helper with no counterpart in the reference: `blocks` work-groups of 256
  * threads each issue `iters` rounds of four independent fp16 32x32x16 MFMAs per
  * wavefront.  ticks (2*blocks uint64) receives, per work-group, the shader-clock and the
