@@ -1,8 +1,11 @@
-"""Build the gfx950 HIP library ``co_alibi_attn/_lib/libco_alibi.so``.
+"""Build the gfx950 HIP library and its torch operators.
 
-Each ``csrc/*.hip`` file is compiled to an object with hipcc (in parallel),
-then linked into one shared library that exports the C ABI declared in
-``include/co_alibi.h``.  Run ``python -m co_alibi_attn._build``.
+Each ``csrc/*.hip`` file is compiled to an object with hipcc (in parallel), then
+linked into ``co_alibi_attn/_lib/libco_alibi.so``, which exports the C ABI declared
+in ``include/co_alibi.h``.  ``csrc/torch_ops.cpp`` (host code only) is then compiled
+against torch's headers and libraries into ``co_alibi_attn/_lib/libco_alibi_torch.so``,
+the PyTorch-ROCm operators ``co_alibi::*`` over that C ABI.  Run
+``python -m co_alibi_attn._build``.
 """
 from __future__ import annotations
 
@@ -17,6 +20,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libco_alibi.so")
+TORCH_LIB_PATH = os.path.join(LIB_DIR, "libco_alibi_torch.so")
 ARCH = "gfx950"
 SOURCES = ("coalibi_fwd.hip", "coalibi_bwd.hip", "coalibi_decode.hip", "coalibi_probe.hip", "coalibi_capi.hip")
 
@@ -47,8 +51,25 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{out}")
 
 
+def _torch_ops_cmd(out: str) -> list[str]:
+    """g++ command of the torch operator library (host code: torch headers, HIP runtime headers)."""
+    import torch.utils.cpp_extension as ce
+
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    abi = int(__import__("torch")._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}"]
+    cmd += [f"-I{p}" for p in ce.include_paths()] + [f"-I{os.path.join(rocm, 'include')}"]
+    cmd += [os.path.join(CSRC, "torch_ops.cpp"), "-o", out]
+    cmd += [f"-L{p}" for p in ce.library_paths()]
+    cmd += ["-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-ltorch", f"-L{LIB_DIR}", "-lco_alibi",
+            "-Wl,-rpath,$ORIGIN"]
+    return cmd
+
+
 def build(verbose: bool = False) -> str:
-    """Compile every source and link the library; returns its path."""
+    """Compile every source and link the library, then the torch operators; returns the library's path."""
     hipcc = _hipcc()
     os.makedirs(OBJ_DIR, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
@@ -69,6 +90,13 @@ def build(verbose: bool = False) -> str:
     if verbose:
         print(" ".join(link), flush=True)
         print(f"built {LIB_PATH}", flush=True)
+    tmp = TORCH_LIB_PATH + ".tmp"
+    cmd = _torch_ops_cmd(tmp)
+    _run(cmd)
+    os.replace(tmp, TORCH_LIB_PATH)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+        print(f"built {TORCH_LIB_PATH}", flush=True)
     return LIB_PATH
 
 

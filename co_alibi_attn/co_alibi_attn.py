@@ -41,17 +41,17 @@ _DEVICE_SLOPES: dict = {}
 
 
 def _device_slopes(n_heads: int, bias_max: float, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
-    """The penalty slopes 2 * _get_coalibi_slopes(n_heads, bias_max) rounded to ``dtype`` on
-    ``device`` (reference co_alibi_attn.py:147), kept per (n_heads, bias_max, dtype, device):
-    a copy from pageable host memory synchronises the stream, which would drain the GPU's
-    queue at every call and make a graph capture fail.  Under torch.compile the values are
-    computed in the traced graph instead."""
+    """The penalty slopes 2 * _get_coalibi_slopes(n_heads, bias_max) rounded to ``dtype`` (reference
+    co_alibi_attn.py:147), held in fp32 on ``device`` -- the form the kernels read, so no call
+    converts them -- and kept per (n_heads, bias_max, dtype, device): a copy from pageable host
+    memory synchronises the stream, which would drain the GPU's queue at every call and make a
+    graph capture fail.  Under torch.compile the values are computed in the traced graph instead."""
     if torch.compiler.is_compiling():
-        return (2.0 * _get_coalibi_slopes(n_heads, bias_max)).to(device, dtype=dtype)
+        return (2.0 * _get_coalibi_slopes(n_heads, bias_max)).to(dtype).to(device, dtype=torch.float32)
     key = (int(n_heads), float(bias_max), dtype, torch.device(device))
     slopes = _DEVICE_SLOPES.get(key)
     if slopes is None:
-        slopes = (2.0 * _get_coalibi_slopes(n_heads, bias_max)).to(device, dtype=dtype)
+        slopes = (2.0 * _get_coalibi_slopes(n_heads, bias_max)).to(dtype).to(device, dtype=torch.float32)
         if type(slopes) is torch.Tensor:  # not a FakeTensor made under a tracing mode
             _DEVICE_SLOPES[key] = slopes
     return slopes
