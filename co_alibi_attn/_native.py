@@ -14,7 +14,7 @@ import torch  # noqa: F401  (must be imported before the HIP library is loaded)
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libco_alibi.so")
 
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
-SUPPORTED_HEAD_DIMS = (32, 64, 128, 256)
+SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 
 # Size of the library-held split-K scratch of co_alibi_decode_noalloc (CO_ALIBI_DECODE_SCRATCH_BYTES).
 DECODE_SCRATCH_BYTES = 32 << 20

@@ -49,9 +49,13 @@ template <typename T, int D>
 struct BwdCfg {
   static constexpr bool kTr = sizeof(T) == 2;
   static constexpr int CH = 16 / sizeof(T);
-  static constexpr int LDR = D + 2 * CH;  // row-major tile stride (b128 row reads and transpose reads)
+  // dQ^T, dK^T and dV^T are produced in 32-row tiles of the head dim: D = 16 runs on a
+  // 32-wide head dim whose upper 16 columns are zero in the LDS tiles the products read
+  // across d (written once, never loaded over).
+  static constexpr int DP = D < 32 ? 32 : D;
+  static constexpr int LDR = DP + 2 * CH;  // row-major tile stride (b128 row reads and transpose reads)
   static constexpr int KS = D / 16;
-  static constexpr int DT = D / 32;
+  static constexpr int DT = DP / 32;
   static constexpr int LDT1 = kBN + CH;   // fp32 pass 1: K^T tile stride
   static constexpr int LDT2 = kBQ<T> + CH;  // fp32 pass 2: Q^T / dO^T tile stride
   static constexpr int LDSP = kTr ? 32 + 2 * CH : 32 + CH;  // per-wave s / dP scratch stride
@@ -138,7 +142,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   using Tile = TileLoader<T, D, kBN, !BwdCfg<T, D>::kTr>;
   __shared__ __align__(16) T sK[kBN * C::LDR];
   __shared__ __align__(16) T sV[kBN * C::LDR];
-  __shared__ __align__(16) T sKt[C::kTr ? 8 : D * C::LDT1];
+  __shared__ __align__(16) T sKt[C::kTr ? 8 : C::DP * C::LDT1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, hh = lane >> 5;
@@ -155,6 +159,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const T* __restrict__ Vp = static_cast<const T*>(args.v) + kvoff;
   const float lam = args.slopes[hq];
   const float lam2 = lam * kLog2e;
+  if constexpr (D < C::DP) {  // padding columns of K (read across d by the dQ product) stay zero
+    lds_zero(sK, (int)sizeof(sK), tid, 256);
+    if constexpr (!C::kTr) lds_zero(sKt, (int)sizeof(sKt), tid, 256);
+  }
 
   const int q0 = qb * kBM;
   const int wrow0 = q0 + wave * 32;
@@ -256,6 +264,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        if (dt * 32 + g * 8 >= D) continue;  // padding rows of dQ^T (D = 16)
         f32x4 v4 = {acc[dt][g * 4 + 0] * sc, acc[dt][g * 4 + 1] * sc, acc[dt][g * 4 + 2] * sc,
                     acc[dt][g * 4 + 3] * sc};
         *reinterpret_cast<vec4*>(dQr + dt * 32 + g * 8 + hh * 4) = __builtin_convertvector(v4, vec4);
@@ -279,8 +288,8 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
   using Tile = TileLoader<T, D, BQ, !BwdCfg<T, D>::kTr>;
   __shared__ __align__(16) T sQ[BQ * C::LDR];
   __shared__ __align__(16) T sdO[BQ * C::LDR];
-  __shared__ __align__(16) T sQt[C::kTr ? 8 : D * C::LDT2];
-  __shared__ __align__(16) T sdOt[C::kTr ? 8 : D * C::LDT2];
+  __shared__ __align__(16) T sQt[C::kTr ? 8 : C::DP * C::LDT2];
+  __shared__ __align__(16) T sdOt[C::kTr ? 8 : C::DP * C::LDT2];
   __shared__ __align__(16) T sSP[4][2][32 * C::LDSP];  // per wavefront: s and dP, [q][key] (fp32: [key][q])
   __shared__ __align__(16) float sLse2[BQ];
   __shared__ __align__(16) float sDsum[BQ];
@@ -302,6 +311,14 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
   const int key0 = kw0 + hh * 16;          // key of register 0 of this lane
   T* __restrict__ sS = sSP[wave][0];
   T* __restrict__ sP = sSP[wave][1];
+  if constexpr (D < C::DP) {  // padding columns of Q and dO (read across d by phase B) stay zero
+    lds_zero(sQ, (int)sizeof(sQ), tid, 256);
+    lds_zero(sdO, (int)sizeof(sdO), tid, 256);
+    if constexpr (!C::kTr) {
+      lds_zero(sQt, (int)sizeof(sQt), tid, 256);
+      lds_zero(sdOt, (int)sizeof(sdOt), tid, 256);
+    }
+  }
 
   vec8 ka[C::KS], va[C::KS];
   {
@@ -457,6 +474,7 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
     for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        if (dt * 32 + g * 8 >= D) continue;  // padding rows of dK^T / dV^T (D = 16)
         const int c0 = dt * 32 + g * 8 + hh * 4;
         f32x4 k4 = {dk[dt][g * 4 + 0] * sc, dk[dt][g * 4 + 1] * sc, dk[dt][g * 4 + 2] * sc,
                     dk[dt][g * 4 + 3] * sc};
@@ -735,14 +753,17 @@ hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream) {
   template hipError_t launch_bwd<T, D, true>(const BwdArgs&, int, hipStream_t); \
   template hipError_t launch_bwd<T, D, false>(const BwdArgs&, int, hipStream_t);
 
+COALIBI_INST_BWD(_Float16, 16)
 COALIBI_INST_BWD(_Float16, 32)
 COALIBI_INST_BWD(_Float16, 64)
 COALIBI_INST_BWD(_Float16, 128)
 COALIBI_INST_BWD(_Float16, 256)
+COALIBI_INST_BWD(__bf16, 16)
 COALIBI_INST_BWD(__bf16, 32)
 COALIBI_INST_BWD(__bf16, 64)
 COALIBI_INST_BWD(__bf16, 128)
 COALIBI_INST_BWD(__bf16, 256)
+COALIBI_INST_BWD(float, 16)
 COALIBI_INST_BWD(float, 32)
 COALIBI_INST_BWD(float, 64)
 COALIBI_INST_BWD(float, 128)

@@ -38,9 +38,9 @@ int check_shape(const char* fn, int dtype, const Shape& s) {
     return fail(CO_ALIBI_EINVAL, std::string(fn) + ": batch, heads and sequence lengths must be >= 1");
   if (s.Hq % s.Hkv != 0)
     return fail(CO_ALIBI_EINVAL, std::string(fn) + ": heads_q must be a multiple of heads_kv");
-  if (s.D != 32 && s.D != 64 && s.D != 128 && s.D != 256)
+  if (s.D != 16 && s.D != 32 && s.D != 64 && s.D != 128 && s.D != 256)
     return fail(CO_ALIBI_EUNSUPPORTED,
-                std::string(fn) + ": head_dim must be 32, 64, 128 or 256, got " + std::to_string(s.D));
+                std::string(fn) + ": head_dim must be 16, 32, 64, 128 or 256, got " + std::to_string(s.D));
   // fp32 tiles at D = 256 exceed the register file in backward pass 2 (fragments and
   // accumulators of 32 keys x 256 dims in fp32).
   if (s.D == 256 && dtype == CO_ALIBI_F32)
@@ -74,6 +74,7 @@ hipError_t fwd_dispatch_causal(const coalibi::FwdArgs& a, bool causal, hipStream
 template <typename T>
 hipError_t fwd_dispatch_d(const coalibi::FwdArgs& a, int D, bool causal, hipStream_t st) {
   switch (D) {
+    case 16: return fwd_dispatch_causal<T, 16>(a, causal, st);
     case 32: return fwd_dispatch_causal<T, 32>(a, causal, st);
     case 64: return fwd_dispatch_causal<T, 64>(a, causal, st);
     case 256:
@@ -91,6 +92,7 @@ hipError_t bwd_dispatch_causal(const coalibi::BwdArgs& a, bool causal, int stage
 template <typename T>
 hipError_t bwd_dispatch_d(const coalibi::BwdArgs& a, int D, bool causal, int stages, hipStream_t st) {
   switch (D) {
+    case 16: return bwd_dispatch_causal<T, 16>(a, causal, stages, st);
     case 32: return bwd_dispatch_causal<T, 32>(a, causal, stages, st);
     case 64: return bwd_dispatch_causal<T, 64>(a, causal, stages, st);
     case 256:
@@ -340,6 +342,12 @@ int decode_impl(const char* fn, bool scratch_ws, int dtype, const void* q, const
   const Shape s{batch, heads_q, heads_kv, 1, seq_kv, head_dim};
   int rc;
   if ((rc = check_shape(fn, dtype, s))) return rc;
+  // The decode kernels read K in pairs of 16-element fragments; a head dim of 16 is one.  The
+  // torch operator co_alibi::decode pads such heads to 32 with zero columns, which changes no
+  // product.
+  if (head_dim == 16)
+    return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": head_dim 16 has no decode kernel (pad q and the "
+                                                         "caches to 32 with zeros)");
   if (heads_q / heads_kv > coalibi::kMaxDecodeGroup)
     return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": at most " + std::to_string(coalibi::kMaxDecodeGroup) +
                                            " query heads per kv head");

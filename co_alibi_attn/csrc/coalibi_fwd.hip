@@ -38,13 +38,16 @@ template <typename T, int D>
 struct FwdCfg {
   static constexpr bool kTr = sizeof(T) == 2;  // V through LDS transpose reads
   static constexpr int CH = 16 / sizeof(T);
+  // O^T is produced in 32-row tiles of the head dim: D = 16 runs on a 32-wide head dim whose
+  // upper 16 columns of V are zero in LDS (written once, never loaded over).
+  static constexpr int DP = D < 32 ? 32 : D;
   static constexpr int LDK = D + CH;       // sK row stride (elements)
   // sV: row-major [key][d] (stride keeps each 4-row transpose read on distinct
   // banks) or, in fp32 mode, transposed [d][key].
-  static constexpr int LDV = kTr ? D + 2 * CH : kFwdBN + CH;
-  static constexpr int V_ELEMS = kTr ? kFwdBN * LDV : D * LDV;
+  static constexpr int LDV = kTr ? DP + 2 * CH : kFwdBN + CH;
+  static constexpr int V_ELEMS = kTr ? kFwdBN * LDV : DP * LDV;
   static constexpr int KS = D / 16;        // k16 steps over the head dim
-  static constexpr int DT = D / 32;        // 32-row tiles of O^T
+  static constexpr int DT = DP / 32;       // 32-row tiles of O^T
 };
 
 template <bool MASKED, bool CAUSAL>
@@ -186,6 +189,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const T* __restrict__ Vp = static_cast<const T*>(args.v) + kvoff;
   const float lam2 = args.slopes[hq] * kLog2e;
   const float sc2 = args.sc2;
+  if constexpr (D < C::DP) {  // the padding columns of V stay zero: tiles only write the D real ones
+    lds_zero(sV, (int)sizeof(sV), tid, 256);
+  }
 
   const int q0 = qb * kFwdBM;
   const int wrow0 = q0 + wave * 32;
@@ -273,6 +279,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        if (dt * 32 + g * 8 >= D) continue;  // padding rows of O^T (D = 16)
         f32x4 v4 = {acc[dt][g * 4 + 0] * inv, acc[dt][g * 4 + 1] * inv, acc[dt][g * 4 + 2] * inv,
                     acc[dt][g * 4 + 3] * inv};
         *reinterpret_cast<vec4*>(Orow + dt * 32 + g * 8 + hh * 4) = __builtin_convertvector(v4, vec4);
@@ -297,14 +304,17 @@ hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
   template hipError_t launch_fwd<T, D, true>(const FwdArgs&, hipStream_t); \
   template hipError_t launch_fwd<T, D, false>(const FwdArgs&, hipStream_t);
 
+COALIBI_INST_FWD(_Float16, 16)
 COALIBI_INST_FWD(_Float16, 32)
 COALIBI_INST_FWD(_Float16, 64)
 COALIBI_INST_FWD(_Float16, 128)
 COALIBI_INST_FWD(_Float16, 256)
+COALIBI_INST_FWD(__bf16, 16)
 COALIBI_INST_FWD(__bf16, 32)
 COALIBI_INST_FWD(__bf16, 64)
 COALIBI_INST_FWD(__bf16, 128)
 COALIBI_INST_FWD(__bf16, 256)
+COALIBI_INST_FWD(float, 16)
 COALIBI_INST_FWD(float, 32)
 COALIBI_INST_FWD(float, 64)
 COALIBI_INST_FWD(float, 128)

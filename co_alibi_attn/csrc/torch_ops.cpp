@@ -154,6 +154,14 @@ std::tuple<Tensor, Tensor> decode_hip(const Tensor& q_in, const Tensor& k_in, co
     return {o, lse};
   }
   c10::hip::HIPGuard guard(q_in.device().index());
+  if (head_dim == 16) {
+    // The decode kernels have no head dim of 16: run on heads padded to 32 with zero columns
+    // (the products over d are unchanged, the padding columns of O come out zero) and return
+    // the first 16 columns.  This copies the caches once per step.
+    auto [o32, lse] = decode_hip(at::constant_pad_nd(q_in, {0, 16}), at::constant_pad_nd(k_in, {0, 16}),
+                                 at::constant_pad_nd(v_in, {0, 16}), slopes, seq_lens, max_seq_len, sm_scale, with_lse);
+    return {o32.narrow(3, 0, 16).contiguous(), lse};
+  }
   const Tensor q = aligned(q_in), k = aligned(k_in), v = aligned(v_in);
   Tensor lens;
   if (seq_lens.has_value() && seq_lens->defined()) lens = seq_lens->to(q.device(), at::kInt).contiguous();

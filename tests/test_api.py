@@ -53,7 +53,8 @@ def _fwd(lib, **over):
     (dict(q=None), 1, "q is NULL"),
     (dict(k=24), 1, "k is not 16-byte aligned"),
     (dict(lse=2), 1, "lse is not 4-byte aligned"),
-    (dict(D=96), 2, "head_dim must be 32, 64, 128 or 256"),
+    (dict(D=96), 2, "head_dim must be 16, 32, 64, 128 or 256"),
+    (dict(D=8), 2, "head_dim must be 16, 32, 64, 128 or 256"),
     (dict(D=256, dtype=0), 2, "head_dim 256 needs fp16 or bf16"),
     (dict(dtype=7), 2, "dtype must be"),
     (dict(Hq=3, Hkv=2), 1, "multiple of heads_kv"),
@@ -142,7 +143,8 @@ def _decode(lib, **over):
     (dict(L=(1 << 21) + 1, cap=1 << 22), 1, "seq_kv above 2097152"),
     (dict(Hq=66, Hkv=1), 2, "at most 32 query heads per kv head"),
     (dict(Hq=6, Hkv=4), 1, "multiple of heads_kv"),
-    (dict(D=80), 2, "head_dim must be 32, 64, 128 or 256"),
+    (dict(D=80), 2, "head_dim must be 16, 32, 64, 128 or 256"),
+    (dict(D=16), 2, "head_dim 16 has no decode kernel"),
     (dict(L=0), 1, ">= 1"),
     (dict(scale=float("inf")), 1, "sm_scale must be finite"),
 ])

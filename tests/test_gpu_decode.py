@@ -53,6 +53,7 @@ CASES = [
     (1, 32, 1, 700, 768, 64),       # group of 32 (every MFMA column)
     (2, 16, 16, 257, 300, 128),     # no grouping, one key past a chunk
     (1, 32, 8, 4113, 4113, 128),    # Llama-style 4:1 grouping, ragged tail
+    (2, 8, 2, 700, 1024, 16),       # head dim 16 (the operator pads the heads to 32)
 ]
 # Head dim 256 (fp16 / bf16 only).
 CASES_D256 = [

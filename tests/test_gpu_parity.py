@@ -127,6 +127,9 @@ CASES = [
     (1, 2, 2, 300, 300, 64, True),      # several key tiles, partial last tile
     (1, 4, 2, 150, 150, 32, True),      # head dim 32, grouped heads
     (1, 2, 2, 90, 200, 32, False),      # head dim 32, non-causal, rectangular
+    (2, 4, 2, 260, 260, 16, True),      # head dim 16 (a 32-wide head dim with zero padding), grouped
+    (1, 3, 3, 70, 190, 16, False),      # head dim 16, non-causal, rectangular, tails
+    (1, 8, 1, 129, 129, 16, True),      # head dim 16, 8 query heads per key head
 ]
 
 
