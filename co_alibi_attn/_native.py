@@ -81,7 +81,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.co_alibi_abi_version() != 1:
+        if handle.co_alibi_abi_version() != 2:
             raise RuntimeError("co_alibi_attn: native library ABI version mismatch")
         _lib = handle
     return _lib

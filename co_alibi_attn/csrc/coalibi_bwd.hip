@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const int col = lane & 31, hh = lane >> 5;
   const int Sq = args.Sq, Skv = args.Skv;
   const int nQB = (Sq + kBM - 1) / kBM;
-  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hq);
+  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hq, 1);
   const int bh = item.head;
   const int qb = nQB - 1 - item.rank;  // rank 0: the longest causal rows
   const int b = bh / args.Hq, hq = bh - b * args.Hq;
@@ -194,10 +194,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
 
   const int last_key = CAUSAL ? min(q0 + kBM - 1, Skv - 1) : Skv - 1;
   const int nkt = last_key / kBN + 1;
+  // Keys left of the forward's first processed key are skipped (their dA and dP are below
+  // 2^-64 of the row's scale, coalibi_kernels.h); the prefix C starts at zero there.
+  static_assert(kBM == kSkipRows, "kstart entries are per pass-1 row block");
+  const int kt0 = args.kstart[(size_t)bh * nQB + qb] / kBN;
 
   Tile kregs, vregs;
-  kregs.load(Kp, 0, Skv, tid);
-  vregs.load(Vp, 0, Skv, tid);
+  kregs.load(Kp, kt0 * kBN, Skv, tid);
+  vregs.load(Vp, kt0 * kBN, Skv, tid);
 
   f32x16 acc[C::DT];
 #pragma unroll
@@ -206,7 +210,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const float* __restrict__ zb_row = args.zb + (size_t)bh * args.nZB * Sq + row;
   float* __restrict__ cb_row = args.cb + (size_t)bh * args.nZB * Sq + row;
 
-  for (int kt = 0; kt < nkt; ++kt) {
+  for (int kt = kt0; kt < nkt; ++kt) {
     __syncthreads();
     kregs.store_rows(sK, C::LDR, tid);
     vregs.store_rows(sV, C::LDR, tid);
@@ -300,7 +304,10 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
   const int col = lane & 31, hh = lane >> 5;
   const int Sq = args.Sq, Skv = args.Skv;
   const int nKB = (Skv + kBK - 1) / kBK;
-  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hkv);
+  static_assert(sizeof(sQ) >= 2 * kMaxBalancedHeads * 4, "the head order is built in sQ");
+  const WorkItem item = balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
+                                      reinterpret_cast<float*>(sQ), reinterpret_cast<int*>(sQ) + kMaxBalancedHeads,
+                                      tid, 256);
   const int bhk = item.head;               // b * Hkv + hkv
   const int kb = item.rank;                // rank 0: key block 0, seen by the most query rows
   const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;
@@ -346,6 +353,7 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
   // Work list: (query head gi, query tile qt) pairs, prefetched one ahead.  Query tiles
   // run from the last one down, so the key blocks of a head that run together read
   // the same Q / dO tiles at about the same time (shared through L2).
+  const int nSkipQB = (Sq + kSkipRows - 1) / kSkipRows;  // kstart entries per query head
   const int nQT = (Sq + BQ - 1) / BQ;
   const int qt0 = CAUSAL ? min((kb * kBK) / BQ, nQT) : 0;
   const int per_head = nQT - qt0;
@@ -394,6 +402,9 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
     __syncthreads();
     if (w + 1 < nwork) prefetch(w + 1);
     if (kw0 >= Skv) continue;
+    // This wavefront's 32 keys lie left of the forward's first processed key for the
+    // tile's row block (a multiple of 64): skipped, with no zb written for them.
+    if (kw0 < args.kstart[(size_t)(b * args.Hq + hq) * nSkipQB + (q0 / kSkipRows)]) continue;
 #pragma unroll
     for (int sq = 0; sq < BQ / 32; ++sq) {
       const int qs0 = q0 + sq * 32;
@@ -531,7 +542,10 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   const int col = lane & 31, hh = lane >> 5;
   const int kg = wave >> 1, qh = wave & 1;
   const int Sq = args.Sq, Skv = args.Skv;
-  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hkv);
+  static_assert(sizeof(sSP) >= 2 * kMaxBalancedHeads * 4, "the head order is built in sSP");
+  const WorkItem item = balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
+                                      reinterpret_cast<float*>(&sSP[0][0][0]),
+                                      reinterpret_cast<int*>(&sSP[0][0][0]) + kMaxBalancedHeads, tid, 64 * kPairWaves);
   const int bhk = item.head;               // b * Hkv + hkv
   const int kb = item.rank;                // rank 0: key block 0, seen by the most query rows
   const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;
@@ -580,11 +594,37 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   Dma dma;  // the Q and dO tiles share the chunk layout
   dma.init(wave, lane);
 
-  // Work list: (query head gi, query tile qt) pairs.
+  // Work list: (query head gi, query tile qt) pairs, qt from qt_hi(gi) down to qt0.
+  // Tail skip: kstart, the first key the forward processed for a 128-row block, is a
+  // multiple of 64, so for every tile this block's 64 keys are processed or skipped as a
+  // whole.  qt_hi(gi) is the last tile of head gi whose row block processed them (found
+  // once, in LDS, for up to kMaxPairGroup query heads per key head; all tiles otherwise),
+  // and a tile inside the range whose row block skipped them is left out by half_live.
+  static_assert(BQ * 2 == kSkipRows, "two query tiles per kstart row block");
+  constexpr int kMaxPairGroup = 64;
+  __shared__ int sQtHi[kMaxPairGroup];
   const int nQT = (Sq + BQ - 1) / BQ;
   const int qt0 = CAUSAL ? min((kb * kPairBK) / BQ, nQT) : 0;
-  const int per_head = nQT - qt0;
-  const int nwork = per_head * group;
+  const int nSkipQB = (Sq + kSkipRows - 1) / kSkipRows;
+  const int kwg0 = kb * kPairBK;
+  const int* __restrict__ kstart_g = args.kstart + (size_t)(b * args.Hq + hkv * group) * nSkipQB;
+  const bool ranged = group <= kMaxPairGroup;
+  if (ranged) {
+    for (int g = tid; g < group; g += 64 * kPairWaves) sQtHi[g] = qt0 - 1;
+    __syncthreads();
+    for (int i = tid; i < group * nSkipQB; i += 64 * kPairWaves) {
+      const int g = i / nSkipQB, rb = i - g * nSkipQB;
+      if (kstart_g[i] <= kwg0) atomicMax(&sQtHi[g], min(2 * rb + 1, nQT - 1));
+    }
+    __syncthreads();
+  }
+  auto qt_hi = [&](int g) { return ranged ? sQtHi[g] : nQT - 1; };
+  auto next_head = [&](int g) {  // the first head from g on with a tile in range, or group
+    while (g < group && qt_hi(g) < qt0) ++g;
+    return g;
+  };
+  int nwork = 0;
+  for (int g = 0; g < group; ++g) nwork += max(qt_hi(g) - qt0 + 1, 0);
   const int jb = kw0 / 32;  // this key group's 32-key block
   auto issue_tile = [&](int gi, int qt, int buf) {
     const size_t qoff = (size_t)(b * args.Hq + hkv * group + gi) * Sq * D;
@@ -614,21 +654,22 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
     else sCb[buf][kg][lane] = st_b;
   };
 
+  // Query tiles run from the last one down: the key blocks of a head that run together
+  // then read the same Q / dO tiles at about the same time (shared through L2).
+  int gi = next_head(0), qt = gi < group ? qt_hi(gi) : 0;  // current work item; the next one is (gn, qn)
   __syncthreads();  // zeroed tiles before the first DMA lands
   if (nwork > 0) {
-    issue_tile(0, nQT - 1, 0);
-    load_stats(0, nQT - 1);
+    issue_tile(gi, qt, 0);
+    load_stats(gi, qt);
     __builtin_amdgcn_s_waitcnt(0);  // the stats loads have to land before they are stored
     store_stats(0);
   }
 
-  // Query tiles run from the last one down: the key blocks of a head that run together
-  // then read the same Q / dO tiles at about the same time (shared through L2).
-  int gi = 0, qt = nQT - 1;  // current work item; the next one is (gn, qn)
   for (int w = 0; w < nwork; ++w) {
     const int buf = w & 1;  // statistics buffer
     const bool wrap = qt == qt0;
-    const int gn = wrap ? gi + 1 : gi, qn = wrap ? nQT - 1 : qt - 1;
+    const int gn = wrap ? next_head(gi + 1) : gi;
+    const int qn = wrap ? (gn < group ? qt_hi(gn) : 0) : qt - 1;
     const int hq = hkv * group + gi;
     const float lam = args.slopes[hq];
     const float lam2 = lam * kLog2e;
@@ -639,10 +680,12 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
     const T* __restrict__ tQ = sQ[0];
     const T* __restrict__ tdO = sdO[0];
 
-    // Query half h of the tile meets this key group (some pair is visible).
+    // Query half h of the tile meets this key group (some pair is visible) and the
+    // forward processed these keys for the tile's row block.
+    const bool processed = kwg0 >= kstart_g[(size_t)gi * nSkipQB + qt / 2];
     auto half_live = [&](int h) {
       const int qs0 = q0 + h * 32;
-      return keys_ok && qs0 < Sq && (!CAUSAL || qs0 + 31 >= kw0);
+      return processed && keys_ok && qs0 < Sq && (!CAUSAL || qs0 + 31 >= kw0);
     };
     if (half_live(qh)) {
       const int qs0 = q0 + qh * 32;

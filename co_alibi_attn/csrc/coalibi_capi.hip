@@ -25,6 +25,11 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 size_t num_zblocks(int seq_kv) { return (static_cast<size_t>(seq_kv) + 31) / 32; }
 
+// fp32 elements of the zb blocks proper, before the kstart / knorm tails.
+size_t zb_block_numel(int batch, int heads_q, int seq_q, int seq_kv) {
+  return static_cast<size_t>(batch) * heads_q * num_zblocks(seq_kv) * seq_q;
+}
+
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 struct Shape {
@@ -108,13 +113,14 @@ extern "C" {
 
 size_t co_alibi_zb_numel(int batch, int heads_q, int seq_q, int seq_kv) {
   if (batch < 1 || heads_q < 1 || seq_q < 1 || seq_kv < 1) return 0;
-  return static_cast<size_t>(batch) * heads_q * num_zblocks(seq_kv) * seq_q;
+  return zb_block_numel(batch, heads_q, seq_q, seq_kv) +
+         static_cast<size_t>(batch) * heads_q * (coalibi::zb_kstart_count(seq_q) + coalibi::zb_knorm_count(seq_kv));
 }
 
 size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_kv) {
   if (batch < 1 || heads_q < 1 || seq_q < 1 || seq_kv < 1) return 0;
   const size_t rows = static_cast<size_t>(batch) * heads_q * seq_q;
-  return round_up(rows * sizeof(float), 256) + co_alibi_zb_numel(batch, heads_q, seq_q, seq_kv) * sizeof(float);
+  return round_up(rows * sizeof(float), 256) + zb_block_numel(batch, heads_q, seq_q, seq_kv) * sizeof(float);
 }
 
 int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const float* slopes, void* o,
@@ -138,12 +144,18 @@ int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const f
   a.o = o;
   a.lse = lse;
   a.zb = zb;
+  if (zb != nullptr) {  // kstart and knorm follow the zb blocks (coalibi_kernels.h)
+    float* tail = zb + zb_block_numel(batch, heads_q, seq_q, seq_kv);
+    a.kstart = reinterpret_cast<int*>(tail);
+    a.knorm = tail + static_cast<size_t>(batch) * heads_q * coalibi::zb_kstart_count(seq_q);
+  }
   a.B = batch;
   a.Hq = heads_q;
   a.Hkv = heads_kv;
   a.Sq = seq_q;
   a.Skv = seq_kv;
   a.nZB = static_cast<int>(num_zblocks(seq_kv));
+  a.nKC = coalibi::zb_knorm_count(seq_kv);
   a.sc2 = sm_scale * coalibi::kLog2eHost;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
@@ -196,6 +208,7 @@ int bwd_impl(const char* fn, int stages, int dtype, const void* dout, const void
   a.dv = dv;
   a.dsum = static_cast<float*>(workspace);
   a.cb = reinterpret_cast<float*>(static_cast<char*>(workspace) + round_up(rows * sizeof(float), 256));
+  a.kstart = reinterpret_cast<const int*>(zb + zb_block_numel(batch, heads_q, seq_q, seq_kv));
   a.B = batch;
   a.Hq = heads_q;
   a.Hkv = heads_kv;
@@ -439,6 +452,6 @@ int co_alibi_decode_noalloc(int dtype, const void* q, const void* k_cache, const
 
 const char* co_alibi_last_error(void) { return g_last_error.c_str(); }
 
-int co_alibi_abi_version(void) { return 1; }
+int co_alibi_abi_version(void) { return 2; }
 
 }  // extern "C"

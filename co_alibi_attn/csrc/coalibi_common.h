@@ -153,18 +153,71 @@ __device__ __forceinline__ typename Mfma<T>::vec8 zero_vec8() {
   return z;
 }
 
-// Work order of a grid of row or key blocks over `heads` (batch, head) pairs.  Ids are
-// taken rank-major, head-minor, where rank 0 is the block with
-// the most work (the longest causal rows, or the key block seen by the most query rows).
-// The dispatcher hands consecutive work-group ids to the 8 XCDs in turn, so every XCD sees
-// its blocks in decreasing cost (longest-processing-time-first list scheduling keeps the
-// tail short) and, when `heads` is a multiple of 8, all blocks of a head run on one XCD and
-// share its L2.
+// Work order of a grid of row or key blocks over B*H (batch, head) pairs (H query heads
+// for row-block grids, H key heads for key-block grids).  Ids are taken rank-major,
+// head-minor, where rank 0 is the block with the most work (the longest causal rows, or
+// the key block seen by the most query rows); the dispatcher hands consecutive work-group
+// ids to the 8 XCDs in turn, so position j of a rank runs on XCD j mod 8, and every XCD
+// sees its blocks in decreasing cost (longest-processing-time-first list scheduling keeps
+// the tail short).
+//
+// Which head sits at position j balances the XCDs.  The tail skip cuts a head's work by
+// its slope (a larger slope skips more keys), so heads differ in work by up to 30x, and a
+// head kept on one XCD leaves that XCD busy long after the others.  Two orders, chosen by
+// same-box measurement per kernel (headline, gqa and long configs):
+//   lpt_item: the heads of rank r are rotated by r / rotate positions.  With rotate = 1 the
+//     blocks of a head visit the XCDs in turn (the forward and pass 1: each block reads
+//     its own Q rows and a key range, so the XCDs' L2 sharing matters little);
+//   balanced_item: the heads are ranked by their smallest slope (for a key head, over its
+//     query heads; larger first, so lighter first), the (rank, batch) pairs are numbered in
+//     that order and dealt to positions in boustrophedon order over the 8 XCDs (0..7,
+//     7..0, ...), so each XCD serves a mix of light and heavy heads, and runs of
+//     kLptRotateRanks consecutive blocks of a head share an XCD and its L2 (pass 2: the
+//     key blocks of a head read the same Q / dO tiles).  Heads beyond kMaxBalancedHeads keep
+//     their index order.
+constexpr int kLptRotateRanks = 4;
 struct WorkItem {
-  int head;  // b * heads_per_batch + h
+  int head;  // b * H + h
   int rank;  // 0 = most work
 };
-__device__ __forceinline__ WorkItem lpt_item(int id, int heads) { return {id % heads, id / heads}; }
+__device__ __forceinline__ WorkItem lpt_item(int id, int heads, int rotate) {
+  const int rank = id / heads;
+  return {(id - rank * heads + rank / rotate) % heads, rank};
+}
+constexpr int kMaxBalancedHeads = 256;
+// `key` and `order` (kMaxBalancedHeads floats / ints of LDS scratch, free again on return)
+// hold the heads' slopes and rank order; every thread of the work-group calls this (three
+// barriers).
+__device__ __forceinline__ WorkItem balanced_item(int id, int B, int H, const float* __restrict__ slopes,
+                                                  int group, float* key, int* order, int tid, int nthreads) {
+  const int heads = B * H;
+  const int rank = id / heads;
+  int j = id - rank * heads;
+  j = (j + rank / kLptRotateRanks) % heads;
+  if (H > kMaxBalancedHeads) return {j, rank};
+  for (int t = tid; t < H; t += nthreads) {
+    float m = __builtin_inff();
+    for (int g = 0; g < group; ++g) {
+      const float l = slopes[t * group + g];
+      m = fminf(m, l > 0.f ? l : 0.f);  // no skip for a slope <= 0 (or NaN): heaviest
+    }
+    key[t] = m;
+  }
+  __syncthreads();
+  for (int t = tid; t < H; t += nthreads) {
+    const float kt = key[t];
+    int r = 0;
+    for (int u = 0; u < H; ++u) r += (key[u] > kt) || (key[u] == kt && u < t);
+    order[r] = t;
+  }
+  __syncthreads();
+  const int blk = j >> 3, x = j & 7;
+  const bool whole = (blk + 1) * 8 <= heads;  // a partial last block of 8 keeps its order
+  const int n = (whole && (blk & 1)) ? blk * 8 + 7 - x : j;  // number in rank order
+  const int h = order[n / B], b = n - (n / B) * B;
+  __syncthreads();  // the scratch may be reused once every wavefront has read its head
+  return {b * H + h, rank};
+}
 
 }  // namespace coalibi
 

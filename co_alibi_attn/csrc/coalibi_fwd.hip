@@ -164,6 +164,54 @@ __device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __re
   }
 }
 
+// max over each chunk of kNormKeys keys of |k|_2, per key head: the key side of the tail
+// skip's bound.  One work-group per (head, chunk) over B*Hq heads: the buffer has room for
+// B*Hq rows, and rows past the B*Hkv key heads are written as zero, so every element of
+// the forward's statistics is written (deterministic outputs).  The D/CH lanes that hold one key row's 16-byte chunks
+// sum their squares with xor shuffles.  A NaN norm is kept (fmaxf would drop it), so a
+// non-finite key disables the skip for its head.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void coalibi_key_norm_kernel(const T* __restrict__ k, float* __restrict__ knorm,
+                                                               int Skv, int nKC, int nKeyHeads) {
+  constexpr int CH = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  constexpr int CPR = D / CH;              // chunks (lanes) per key row: 2 .. 32
+  constexpr int RPP = 256 / CPR;           // key rows per pass of the work-group
+  static_assert(CPR >= 2 && CPR <= 64 && (CPR & (CPR - 1)) == 0, "a key row spans a power-of-two lane group");
+  const int bhk = blockIdx.x / nKC, c = blockIdx.x - bhk * nKC;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (bhk >= nKeyHeads) {
+    if (tid == 0) knorm[(size_t)bhk * nKC + c] = 0.f;
+    return;
+  }
+  const T* __restrict__ base = k + (size_t)bhk * Skv * D;
+  const int r1 = min((c + 1) * kNormKeys, Skv);
+  float best = 0.f;
+  for (int r = c * kNormKeys + tid / CPR; r < r1; r += RPP) {
+    const typename VecOf<T, CH>::type x =
+        __builtin_bit_cast(typename VecOf<T, CH>::type, ld16(base + (size_t)r * D + (tid % CPR) * CH));
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < CH; ++e) ss = fmaf((float)x[e], (float)x[e], ss);
+#pragma unroll
+    for (int off = CPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    best = ss != ss ? ss : fmaxf(best, ss);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float o = __shfl_xor(best, off);
+    best = o != o ? o : fmaxf(best, o);
+  }
+  __shared__ float red[4];
+  if (lane == 0) red[wave] = best;
+  __syncthreads();
+  if (tid == 0) {
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) m = red[w] != red[w] ? red[w] : fmaxf(m, red[w]);
+    knorm[(size_t)bhk * nKC + c] = sqrtf(m);
+  }
+}
+
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coalibi_fwd_kernel(FwdArgs args) {
   using C = FwdCfg<T, D>;
@@ -178,7 +226,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const int col = lane & 31, hh = lane >> 5;
   const int Sq = args.Sq, Skv = args.Skv;
   const int nQB = (Sq + kFwdBM - 1) / kFwdBM;
-  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hq);
+  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hq, 1);
   const int bh = item.head;
   const int qb = nQB - 1 - item.rank;  // rank 0: the longest causal rows
   const int b = bh / args.Hq, hq = bh - b * args.Hq;
@@ -209,6 +257,38 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   }
   const float tile_sc2 = kPreScaled ? 1.0f : sc2;
 
+  // Tail skip (coalibi_kernels.h): this row's bound on |t| in log2 units, |q| * max|k| with
+  // the scale (folded into q in 16-bit types), with a margin for the rounding of the norms
+  // and of the fp32 dot products.
+  // The bound stays in LDS (one per row) rather than in a register across the tile loop.
+  __shared__ float sKmax[4];
+  __shared__ float sBound[kFwdBM];
+  __shared__ int sDone[4];
+  const bool tail_skip = args.kstart != nullptr && lam2 > 0.f;
+  if (tail_skip) {
+    float qq = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qq = fmaf((float)qf[ks][e], (float)qf[ks][e], qq);
+    qq += other_half(qq);
+    const float* kn = args.knorm + ((size_t)b * args.Hkv + hkv) * args.nKC;
+    float km = 0.f;
+    for (int c = tid; c < args.nKC; c += 256) km = kn[c] != kn[c] ? kn[c] : fmaxf(km, kn[c]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float o = __shfl_xor(km, off);
+      km = o != o ? o : fmaxf(km, o);
+    }
+    if (lane == 0) sKmax[wave] = km;
+    __syncthreads();
+    km = sKmax[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) km = sKmax[w] != sKmax[w] ? sKmax[w] : fmaxf(km, sKmax[w]);
+    if (hh == 0) sBound[wave * 32 + col] = sqrtf(qq) * km * (kPreScaled ? 1.0f : sc2) * 1.001f + 1e-3f;
+  }
+  int kfirst = 0;  // first key of the leftmost tile processed
+
   const int last_key = CAUSAL ? min(q0 + kFwdBM - 1, Skv - 1) : Skv - 1;
   const int nkt = last_key / kFwdBN + 1;
 
@@ -225,8 +305,18 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const bool write_zb = args.zb != nullptr;
   float* __restrict__ zb_row = write_zb ? args.zb + (size_t)bh * args.nZB * Sq + row : nullptr;
 
-  for (int kt = nkt - 1; kt >= 0; --kt) {
+  int kt_end = 0;  // the loop's lower bound, raised by the tail skip
+  for (int kt = nkt - 1; kt >= kt_end; --kt) {
     __syncthreads();
+    // Every wavefront's rows passed the tail test after tile kt + 1: the keys left of it
+    // carry weights below 2^-kSkipLog2 (the vote is uniform, so all wavefronts leave here).
+    // Leaving through the loop bound rather than a break keeps the loop's register
+    // allocation as it is without the skip (a break costs 13 spilled registers at D = 128).
+    if (tail_skip && kt < nkt - 1 && (sDone[0] & sDone[1] & sDone[2] & sDone[3])) {
+      kfirst = (kt + 1) * kFwdBN;
+      kt_end = kt + 1;
+      continue;
+    }
     kt_regs.store_rows(sK, C::LDK, tid);
     if constexpr (C::kTr)
       vt_regs.template store_rows<false>(sV, C::LDV, tid);
@@ -247,6 +337,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
         kt_regs.load(Kp, (kt - 1) * kFwdBN, Skv, tid);
         vt_regs.load(Vp, (kt - 1) * kFwdBN, Skv, tid);
       }
+      if (tail_skip && lane == 0) sDone[wave] = Sq <= wrow0;  // no visible key yet: only rows past Sq pass
       continue;
     }
     const bool masked = (CAUSAL && k0 + kFwdBN - 1 > wrow0) || (k0 + kFwdBN > Skv);
@@ -265,7 +356,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
       kt_regs.load(Kp, (kt - 1) * kFwdBN, Skv, tid);
       vt_regs.load(Vp, (kt - 1) * kFwdBN, Skv, tid);
     }
+    if (tail_skip) {
+      // Every key left of k0 has z >= zr, so its weight is at most 2^(bound - lam2*zr - m2).
+      const bool done = !row_ok || (m2 != kNegInf && sBound[wave * 32 + col] - lam2 * zr - m2 < -kSkipLog2);
+      const bool all = __all(done);
+      if (lane == 0) sDone[wave] = all;
+    }
   }
+  if (args.kstart != nullptr && tid == 0) args.kstart[(size_t)bh * nQB + qb] = kfirst;
 
   // O = acc / l and LSE = m + log(l) with l = sum_j 2^(a_j - m2) >= 1 (m2 is one of
   // the a_j and at most 8 below their max): the reference's "+1e-9" in l + 1e-9
@@ -294,6 +392,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
 
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
+  static_assert(kFwdBM == kSkipRows, "kstart entries are per forward row block");
+  if (a.kstart != nullptr) {
+    hipLaunchKernelGGL((coalibi_key_norm_kernel<T, D>), dim3(a.nKC * a.B * a.Hq), dim3(256), 0, stream,
+                       static_cast<const T*>(a.k), const_cast<float*>(a.knorm), a.Skv, a.nKC, a.B * a.Hkv);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   const int nQB = (a.Sq + kFwdBM - 1) / kFwdBM;
   const int grid = nQB * a.B * a.Hq;
   hipLaunchKernelGGL((coalibi_fwd_kernel<T, D, CAUSAL>), dim3(grid), dim3(256), 0, stream, a);

@@ -11,7 +11,29 @@ constexpr float kLog2eHost = 1.4426950408889634f;
 // k/v/dk/dv (B, Hkv, Skv, D).  Query head h reads key/value head h / (Hq/Hkv).
 // zb (penalty statistics written by the forward, read by the backward) is
 // (B*Hq, nZB, Sq) fp32 with nZB = ceil(Skv/32): zb[bh][J][i] = sum of
-// sigmoid(p_ik) over valid keys k >= 32*J of row i.
+// sigmoid(p_ik) over valid keys k >= 32*J of row i.  The same buffer continues with
+// two small arrays:
+//   kstart (B*Hq, nQB) int32, nQB = ceil(Sq/128): the first key the forward processed
+//     for each 128-row block.  Every key left of it has a softmax weight below
+//     2^-kSkipLog2 of its row's total in every row of the block (the tail skip below);
+//     the backward passes skip the same keys, and zb of those blocks is not written;
+//   knorm (B*Hq, nKC) fp32, nKC = ceil(Skv/kNormKeys): max_k |k|_2 over each chunk of
+//     kNormKeys keys of key head b*Hkv + h in its first B*Hkv rows, zero in the rest.
+//
+// Tail skip.  In the log2 domain a row's logit for key k is a_k = t_k - lam2 * z_k with
+// t_k = q.k * sm_scale * log2(e) and z_k = sum of sigmoids of the visible keys >= k.  The
+// forward walks keys from the diagonal leftwards, so when it has processed every key from
+// k_next on, z_k >= zr (the sum over those keys) for every k < k_next, as sigmoids are
+// >= 0, and |t_k| <= |q| * max|k| * sm_scale * log2(e) =: bound (Cauchy-Schwarz).  With
+// lam2 > 0 and m2 the running maximum, every later weight 2^(a_k - m2) is then at most
+// 2^(bound - lam2 * zr - m2); once that is below 2^-kSkipLog2 for all rows of a 128-row
+// block the forward stops.  The row total l is >= 1 at the final scale, so each skipped
+// weight is below 2^-kSkipLog2 of it (the softmax probability s = 2^(a - LSE2) too).
+constexpr int kNormKeys = 256;
+constexpr float kSkipLog2 = 64.0f;
+constexpr int kSkipRows = 128;  // rows per kstart entry: the forward's and pass 1's row block
+inline int zb_kstart_count(int Sq) { return (Sq + kSkipRows - 1) / kSkipRows; }
+inline int zb_knorm_count(int Skv) { return (Skv + kNormKeys - 1) / kNormKeys; }
 struct FwdArgs {
   const void* q;
   const void* k;
@@ -20,7 +42,9 @@ struct FwdArgs {
   void* o;
   float* lse;  // (B*Hq, Sq) natural-log log-sum-exp
   float* zb;
-  int B, Hq, Hkv, Sq, Skv, nZB;
+  int* kstart;         // (B*Hq, nQB) or NULL (no tail skip: inference without statistics)
+  const float* knorm;  // (B*Hkv, nKC) chunk maxima of |k|, with kstart
+  int B, Hq, Hkv, Sq, Skv, nZB, nKC;
   float sc2;  // sm_scale * log2(e)
 };
 
@@ -40,6 +64,7 @@ struct BwdArgs {
   void* dv;
   float* dsum;
   float* cb;
+  const int* kstart;  // (B*Hq, nQB): keys left of kstart are skipped (see above)
   int B, Hq, Hkv, Sq, Skv, nZB;
   float sc2;
   float sm_scale;
@@ -74,6 +99,7 @@ struct DecodeArgs {
 // Split-K work-groups the decode aims at per CU: one round of the two that are resident.
 constexpr int kDecodeWGsPerCU = 2;
 
+// Forward; with a.kstart it first launches the key-norm kernel that fills a.knorm.
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 

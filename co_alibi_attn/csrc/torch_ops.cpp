@@ -57,7 +57,8 @@ Tensor slopes_f32(const Tensor& slopes, const Tensor& like) {
 Tensor empty_stats(const Tensor& q) { return at::empty({0}, q.options().dtype(at::kFloat)); }
 
 int64_t zb_numel(int64_t batch, int64_t heads_q, int64_t seq_q, int64_t seq_kv) {
-  return batch * heads_q * ((seq_kv + 31) / 32) * seq_q;
+  return static_cast<int64_t>(co_alibi_zb_numel(static_cast<int>(batch), static_cast<int>(heads_q),
+                                                static_cast<int>(seq_q), static_cast<int>(seq_kv)));
 }
 
 hipStream_t current_stream(const Tensor& t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }

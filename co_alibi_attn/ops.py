@@ -34,29 +34,50 @@ __all__ = ["fwd", "bwd", "bwd_dq", "backward_for", "decode", "zb_numel", "TORCH_
 TORCH_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libco_alibi_torch.so")
 
 
-def _load() -> None:
-    """Load the C++ operators (once); there is no Python fallback."""
+def _load() -> str | None:
+    """Load the C++ operators (once); returns why they are unavailable, or None.  There is
+    no Python fallback: without them every operator raises (so the package still imports,
+    as the build itself needs)."""
     if hasattr(torch.ops.co_alibi, "fwd"):
-        return
+        return None
     if not os.path.exists(TORCH_LIB_PATH):
-        raise RuntimeError(f"co_alibi_attn: torch operator library {TORCH_LIB_PATH} is not built; "
-                           "run `python -m co_alibi_attn._build`")
-    _native.lib()  # the C-ABI library the operators call, with its ABI version check
+        return (f"co_alibi_attn: torch operator library {TORCH_LIB_PATH} is not built; "
+                "run `python -m co_alibi_attn._build`")
+    try:
+        _native.lib()  # the C-ABI library the operators call, with its ABI version check
+    except RuntimeError as e:
+        return str(e)
     torch.ops.load_library(TORCH_LIB_PATH)
+    return None
 
 
-_load()
+_MISSING = _load()
 
-fwd = torch.ops.co_alibi.fwd
-bwd = torch.ops.co_alibi.bwd
-bwd_dq = torch.ops.co_alibi.bwd_dq
-decode = torch.ops.co_alibi.decode
+
+def require() -> None:
+    """Raise the reason the operators are unavailable, if they are."""
+    if _MISSING is not None:
+        raise RuntimeError(_MISSING)
+
+
+def _unavailable(*args, **kwargs):
+    require()
+
+
+if _MISSING is None:
+    fwd = torch.ops.co_alibi.fwd
+    bwd = torch.ops.co_alibi.bwd
+    bwd_dq = torch.ops.co_alibi.bwd_dq
+    decode = torch.ops.co_alibi.decode
+else:
+    fwd = bwd = bwd_dq = decode = _unavailable
 
 
 def zb_numel(batch: int, heads_q: int, seq_q: int, seq_kv: int) -> int:
-    """fp32 elements of the forward's penalty statistics: B*Hq * ceil(Skv/32) * Sq
-    (the value co_alibi_zb_numel of the C ABI returns)."""
-    return batch * heads_q * ((seq_kv + 31) // 32) * seq_q
+    """fp32 elements of the forward's penalty statistics (the value co_alibi_zb_numel of
+    the C ABI returns): B*Hq * (ceil(Skv/32) * Sq  zb blocks, + ceil(Sq/128)  first
+    processed key per 128-row block, + ceil(Skv/256)  key-norm chunk maxima)."""
+    return batch * heads_q * (((seq_kv + 31) // 32) * seq_q + (seq_q + 127) // 128 + (seq_kv + 255) // 256)
 
 
 def _empty_stats(q: Tensor) -> Tensor:
@@ -78,38 +99,42 @@ def backward_for(needs_input_grad, do, q, k, v, o, lse, zb, slopes, causal, sm_s
 # ------------------------------------------------------------------ shape functions
 
 
-@torch.library.register_fake("co_alibi::fwd")
-def _fwd_fake(q, k, v, slopes, causal, sm_scale, with_stats):
-    """o (B, Hq, Sq, D) in q.dtype; with_stats: lse (B, Hq, Sq) and zb (B*Hq*ceil(Skv/32)*Sq,)
-    in fp32, else both empty.  Causal zb entries of 32-key blocks wholly past a row's diagonal
-    are left unwritten by the kernel; no reader needs them."""
-    batch, heads_q, seq_q, _ = q.shape
-    o = torch.empty_like(q, memory_format=torch.contiguous_format)
-    if not with_stats:
-        return o, _empty_stats(q), _empty_stats(q)
-    lse = q.new_empty((batch, heads_q, seq_q), dtype=torch.float32)
-    zb = q.new_empty((zb_numel(batch, heads_q, seq_q, k.shape[2]),), dtype=torch.float32)
-    return o, lse, zb
+def _register_fakes() -> None:
+    """Shape functions of the four operators (FakeTensor / meta tracing, torch.compile)."""
+
+    @torch.library.register_fake("co_alibi::fwd")
+    def _fwd_fake(q, k, v, slopes, causal, sm_scale, with_stats):
+        """o (B, Hq, Sq, D) in q.dtype; with_stats: lse (B, Hq, Sq) and zb (zb_numel(...),) in
+        fp32, else both empty.  Causal zb entries of 32-key blocks wholly past a row's diagonal
+        are left unwritten by the kernel; no reader needs them."""
+        batch, heads_q, seq_q, _ = q.shape
+        o = torch.empty_like(q, memory_format=torch.contiguous_format)
+        if not with_stats:
+            return o, _empty_stats(q), _empty_stats(q)
+        lse = q.new_empty((batch, heads_q, seq_q), dtype=torch.float32)
+        zb = q.new_empty((zb_numel(batch, heads_q, seq_q, k.shape[2]),), dtype=torch.float32)
+        return o, lse, zb
+
+    @torch.library.register_fake("co_alibi::bwd")
+    def _bwd_fake(do, q, k, v, o, lse, zb, slopes, causal, sm_scale):
+        """(dq, dk, dv) in the input dtype; dk / dv have k's head count (summed over each group)."""
+        cf = torch.contiguous_format
+        return (torch.empty_like(q, memory_format=cf), torch.empty_like(k, memory_format=cf),
+                torch.empty_like(v, memory_format=cf))
+
+    @torch.library.register_fake("co_alibi::bwd_dq")
+    def _bwd_dq_fake(do, q, k, v, o, lse, zb, slopes, causal, sm_scale):
+        """dq alone (backward pass 1), bit-identical to co_alibi::bwd's dq."""
+        return torch.empty_like(q, memory_format=torch.contiguous_format)
+
+    @torch.library.register_fake("co_alibi::decode")
+    def _decode_fake(q, k_cache, v_cache, slopes, seq_lens, max_seq_len, sm_scale, with_lse):
+        """o (B, Hq, 1, D) in q.dtype and, with with_lse, the natural-log LSE (B, Hq, 1) in fp32."""
+        batch, heads_q, _, _ = q.shape
+        o = torch.empty_like(q, memory_format=torch.contiguous_format)
+        lse = q.new_empty((batch, heads_q, 1), dtype=torch.float32) if with_lse else _empty_stats(q)
+        return o, lse
 
 
-@torch.library.register_fake("co_alibi::bwd")
-def _bwd_fake(do, q, k, v, o, lse, zb, slopes, causal, sm_scale):
-    """(dq, dk, dv) in the input dtype; dk / dv have k's head count (summed over each group)."""
-    cf = torch.contiguous_format
-    return (torch.empty_like(q, memory_format=cf), torch.empty_like(k, memory_format=cf),
-            torch.empty_like(v, memory_format=cf))
-
-
-@torch.library.register_fake("co_alibi::bwd_dq")
-def _bwd_dq_fake(do, q, k, v, o, lse, zb, slopes, causal, sm_scale):
-    """dq alone (backward pass 1), bit-identical to co_alibi::bwd's dq."""
-    return torch.empty_like(q, memory_format=torch.contiguous_format)
-
-
-@torch.library.register_fake("co_alibi::decode")
-def _decode_fake(q, k_cache, v_cache, slopes, seq_lens, max_seq_len, sm_scale, with_lse):
-    """o (B, Hq, 1, D) in q.dtype and, with with_lse, the natural-log LSE (B, Hq, 1) in fp32."""
-    batch, heads_q, _, _ = q.shape
-    o = torch.empty_like(q, memory_format=torch.contiguous_format)
-    lse = q.new_empty((batch, heads_q, 1), dtype=torch.float32) if with_lse else _empty_stats(q)
-    return o, lse
+if _MISSING is None:
+    _register_fakes()

@@ -46,9 +46,14 @@ enum co_alibi_status {
 };
 
 /* Number of fp32 elements of the penalty statistics `zb` that co_alibi_fwd
- * writes and co_alibi_bwd reads: B*Hq * ceil(Skv/32) * Sq.  zb[bh][J][i] is the
- * sum of sigmoid(sm_scale * q_i.k_j) over the visible keys j >= 32*J of row i.
- * It takes the place of the reference's RowSigTotal (co_alibi_attn.py:37). */
+ * writes and co_alibi_bwd reads: B*Hq * (ceil(Skv/32) * Sq + ceil(Sq/128) +
+ * ceil(Skv/256)).  The first B*Hq*ceil(Skv/32)*Sq are zb[bh][J][i], the sum of
+ * sigmoid(sm_scale * q_i.k_j) over the visible keys j >= 32*J of row i; they take
+ * the place of the reference's RowSigTotal (co_alibi_attn.py:37).  Then, per
+ * 128-row block, the first key the forward processed (keys further left carry
+ * softmax weights below 2^-64 of their row's total and are skipped by forward and
+ * backward alike; zb is not written for them), and per 256-key chunk of each key
+ * head, the largest |k|. */
 size_t co_alibi_zb_numel(int batch, int heads_q, int seq_q, int seq_kv);
 
 /* Bytes of device scratch co_alibi_bwd needs. */
@@ -136,7 +141,7 @@ int co_alibi_probe_mfma(void* ticks, void* sink, int blocks, int iters, void* st
 /* Message describing the last failed call on this thread ("" if none). */
 const char* co_alibi_last_error(void);
 
-/* ABI version of this header: 1. */
+/* ABI version of this header: 2 (the zb buffer gained its kstart / knorm tails). */
 int co_alibi_abi_version(void);
 
 #ifdef __cplusplus

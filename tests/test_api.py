@@ -26,14 +26,14 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in co_alibi.h but not exported"
     assert sorted(_native.EXPORTS) == declared
-    assert lib.co_alibi_abi_version() == 1
+    assert lib.co_alibi_abi_version() == 2
 
 
 def test_sizes():
     lib = _native.lib()
-    # zb: B*Hq*ceil(Skv/32)*Sq fp32
-    assert lib.co_alibi_zb_numel(4, 16, 4096, 4096) == 4 * 16 * 128 * 4096
-    assert lib.co_alibi_zb_numel(1, 2, 5, 33) == 1 * 2 * 2 * 5
+    # zb: B*Hq * (ceil(Skv/32)*Sq blocks + ceil(Sq/128) kstart + ceil(Skv/256) key-norm chunks)
+    assert lib.co_alibi_zb_numel(4, 16, 4096, 4096) == 4 * 16 * (128 * 4096 + 32 + 16)
+    assert lib.co_alibi_zb_numel(1, 2, 5, 33) == 1 * 2 * (2 * 5 + 1 + 1)
     assert lib.co_alibi_zb_numel(0, 2, 5, 33) == 0
     rows = 4 * 16 * 4096
     assert lib.co_alibi_bwd_workspace_bytes(4, 16, 4096, 4096) == rows * 4 + 4 * 16 * 128 * 4096 * 4

@@ -35,7 +35,8 @@ def test_opcheck_fwd_bwd(dtype):
     sl, scale = slopes(4, dtype), 1 / 8
     grads = tuple(t.clone().requires_grad_() for t in (q, k, v))
     torch.library.opcheck(torch.ops.co_alibi.fwd, (q, k, v, sl, True, scale, False))
-    # Non-causal: every zb entry is written, so eager and AOT-traced outputs compare in full.
+    # Non-causal at a length the tail skip does not shorten: every entry of zb (and of its
+    # kstart / knorm tails) is written, so eager and AOT-traced outputs compare in full.
     torch.library.opcheck(torch.ops.co_alibi.fwd, (*grads, sl, False, scale, True))
     # Causal: zb entries past the diagonal are unwritten (nothing reads them), so the
     # eager-vs-traced output comparison is left to test_compile_fullgraph_matches_eager.
