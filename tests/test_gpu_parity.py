@@ -232,6 +232,57 @@ def test_inference_forward_equals_training_forward(dtype):
         assert torch.equal(o_abi, o_plain)
 
 
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["fp16", "bf16", "fp32"])
+def test_tail_skip(dtype, causal):
+    """Slopes large enough that the forward stops early (keys whose weight is below 2^-64 of
+    their row's total are left out, and the backward passes leave out the same keys):
+    - the first processed key per 128-row block (the zb tail) is a multiple of 64, positive for
+      the steep heads, zero for the flat one, and no later than the block's diagonal tile;
+    - O equals the forward without statistics, which skips nothing (bit for bit in fp16,
+      where each skipped weight rounds to zero; within 1e-6 in bf16 and fp32);
+    - forward and backward match the oracle, which computes every key, under the parity bar."""
+    lib = _native.lib()
+    B, Hq, Hkv, S, D = 1, 4, 2, 1000, 64
+    q, k, v, do = rand_inputs(B, Hq, Hkv, S, S, D, dtype, seed=21)
+    # Steep slopes concentrate each row's weight on a few keys, so dV_k is close to a few dO
+    # rows; dO at half scale keeps |dV| within the range where the bar applies unscaled.
+    do = (do.float() * 0.5).to(dtype)
+    lam = torch.tensor([4.0, 1.0, 0.25, 1e-3]).to(dtype).float()
+    scale = 1.0 / math.sqrt(D)
+    print(f"tail skip {dtype} causal={causal}", flush=True)
+    qd, kd, vd, dod, lamd = (t.to(DEV) for t in (q, k, v, do, lam))
+    o, lse, zb = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
+    st = torch.cuda.current_stream().cuda_stream
+    o_plain = torch.empty_like(qd)
+    _native.check(lib.co_alibi_fwd(_native.DTYPE_CODES[dtype], qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                   lamd.data_ptr(), o_plain.data_ptr(), 0, 0, B, Hq, Hkv, S, S, D, int(causal),
+                                   scale, st))
+    ws_bytes = lib.co_alibi_bwd_workspace_bytes(B, Hq, S, S)
+    ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    _native.check(lib.co_alibi_bwd(_native.DTYPE_CODES[dtype], dod.data_ptr(), qd.data_ptr(), kd.data_ptr(),
+                                   vd.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), lamd.data_ptr(),
+                                   dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq, Hkv,
+                                   S, S, D, int(causal), scale, st))
+    torch.cuda.synchronize()
+    nzb, nqb = (S + 31) // 32, (S + 127) // 128
+    kstart = zb[B * Hq * nzb * S:B * Hq * (nzb * S + nqb)].view(torch.int32).view(Hq, nqb).cpu()
+    print(f"  first processed key per 128-row block:\n{kstart}", flush=True)
+    assert (kstart % 64 == 0).all() and (kstart >= 0).all()
+    last_tile = torch.tensor([(min(qb * 128 + 127, S - 1) if causal else S - 1) // 64 * 64 for qb in range(nqb)])
+    assert (kstart <= last_tile).all()
+    assert (kstart[0] > 0).sum() >= nqb - 2 and (kstart[3] == 0).all()
+    if dtype == torch.float16:
+        assert torch.equal(o, o_plain)
+    else:
+        assert (o.float() - o_plain.float()).abs().max().item() <= 1e-6
+    ro, _ = ref.forward(q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
+    rdq, rdk, rdv = ref.backward(do.float(), q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
+    assert_parity(tuple(t.float().cpu() for t in (o, dq, dk, dv)), (ro, rdq, rdk, rdv), TOL[dtype],
+                  f"tail skip causal={causal}", dtype)
+
+
 def test_sm_scale_and_bias_max_arguments():
     q, k, v, do = rand_inputs(1, 3, 3, 120, 120, 64, torch.float32, seed=5)
     got = hip_fwd_bwd(q, k, v, do, causal=True, sm_scale=0.3, bias_max=4.0)
