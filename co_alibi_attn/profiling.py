@@ -44,7 +44,9 @@ if __package__ in (None, ""):
 CALIBRATION_BYTES = 1 << 30
 KERNELS = ("coalibi_fwd_kernel", "coalibi_bwd_dq_kernel", "coalibi_bwd_dkdv_kernel")
 DECODE_KERNELS = ("coalibi_decode_split_kernel", "coalibi_decode_merge_kernel")
-NAMED_KERNELS = KERNELS + DECODE_KERNELS
+# co_alibi_fwd launches the key-norm kernel (max |k| per key chunk, for the tail skip) before
+# the forward kernel; per-launch timings of "coalibi_fwd_kernel" through the C ABI include it.
+NAMED_KERNELS = KERNELS + DECODE_KERNELS + ("coalibi_key_norm_kernel",)
 # The two --pmc passes of the counter summary: at most 8 SQ and 2 GRBM counters each.
 COUNTER_PASSES = (
     ("SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU", "SQ_WAVES",
