@@ -557,30 +557,23 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   T* __restrict__ sS = sSP[kg][0];
   T* __restrict__ sP = sSP[kg][1];
 
-  // Zero the tile buffers once: DMA slots past the last query row then hold zeros.
-  lds_zero(&sQ[0][0], (int)sizeof(sQ), tid, 64 * kPairWaves);
-  lds_zero(&sdO[0][0], (int)sizeof(sdO), tid, 64 * kPairWaves);
-
+  // The work-group's reads before its first tile go out together and share one round
+  // trip: K fragments into registers, the V tile by buffer-to-LDS DMA (LDS row R of each
+  // 32-row group holds key kRowOfReg(R) of the group, the A-operand order; keys past Skv
+  // land as zero) and, below, the forward's kstart rows of the group's heads.
   vec8 ka[C::KS];
   {
-    const int key = kw0 + kRowOfReg(col);
-    const bool key_ok = key < Skv;
-    const T* __restrict__ Kr = static_cast<const T*>(args.k) + kvoff + (size_t)key * D;
-    // K pre-scaled by sm_scale*log2(e), so S^T comes out in log2 units.
+    const bool key_ok = kw0 + kRowOfReg(col) < Skv;
+    const T* __restrict__ Kr = static_cast<const T*>(args.k) + kvoff + (size_t)(kw0 + kRowOfReg(col)) * D;
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks)
-      ka[ks] = scale_vec8<T>(key_ok ? ld_vec8(Kr + ks * 16 + hh * 8) : zero_vec8<T>(), args.sc2);
+    for (int ks = 0; ks < C::KS; ++ks) ka[ks] = key_ok ? ld_vec8(Kr + ks * 16 + hh * 8) : zero_vec8<T>();
   }
-  // V rows of the work-group's keys; LDS row R of each 32-row group holds key
-  // kRowOfReg(R) of the group, the A-operand order.
   {
-    const int kbase = kb * kPairBK;
-    const T* __restrict__ Vp = static_cast<const T*>(args.v) + kvoff;
-    for (int g = tid; g < kPairBK * (D / 8); g += 64 * kPairWaves) {
-      const int r = g / (D / 8), c = (g - r * (D / 8)) * 8;
-      const int key = kbase + (r & ~31) + kRowOfReg(r & 31);
-      st16(sV + r * C::LDR + c, key < Skv ? ld16(Vp + (size_t)key * D + c) : u32x4{0u, 0u, 0u, 0u});
-    }
+    using VDma = DmaTile<T, D, kPairBK, C::LDR, kPairWaves, true>;
+    static_assert(VDma::LDS_ELEMS == kPairBK * C::LDR, "the V DMA writes exactly the V tile");
+    VDma vdma;
+    vdma.init(wave, lane);
+    vdma.issue(static_cast<const T*>(args.v) + kvoff, kb * kPairBK, Skv, sV, wave);
   }
   const T* __restrict__ sVg = sV + kg * 32 * C::LDR;
 
@@ -592,6 +585,7 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   }
 
   Dma dma;  // the Q and dO tiles share the chunk layout
+  static_assert(Dma::LDS_ELEMS == TILE, "every DMA writes its whole tile (pad and tail chunks as zero)");
   dma.init(wave, lane);
 
   // Work list: (query head gi, query tile qt) pairs, qt from qt_hi(gi) down to qt0.
@@ -609,15 +603,21 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   const int kwg0 = kb * kPairBK;
   const int* __restrict__ kstart_g = args.kstart + (size_t)(b * args.Hq + hkv * group) * nSkipQB;
   const bool ranged = group <= kMaxPairGroup;
-  if (ranged) {
-    for (int g = tid; g < group; g += 64 * kPairWaves) sQtHi[g] = qt0 - 1;
-    __syncthreads();
-    for (int i = tid; i < group * nSkipQB; i += 64 * kPairWaves) {
-      const int g = i / nSkipQB, rb = i - g * nSkipQB;
-      if (kstart_g[i] <= kwg0) atomicMax(&sQtHi[g], min(2 * rb + 1, nQT - 1));
+  if (ranged) {  // wavefront w finds qt_hi of heads w, w + kPairWaves, ...
+    for (int g = wave; g < group; g += kPairWaves) {
+      int hi = qt0 - 1;
+      for (int rb = lane; rb < nSkipQB; rb += 64)
+        if (kstart_g[(size_t)g * nSkipQB + rb] <= kwg0) hi = max(hi, min(2 * rb + 1, nQT - 1));
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) hi = max(hi, __shfl_xor(hi, off));
+      if (lane == 0) sQtHi[g] = hi;
     }
-    __syncthreads();
   }
+  // K pre-scaled by sm_scale*log2(e), so S^T comes out in log2 units.
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks) ka[ks] = scale_vec8<T>(ka[ks], args.sc2);
+  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's V DMA
+  __syncthreads();                // the V tile and sQtHi
   auto qt_hi = [&](int g) { return ranged ? sQtHi[g] : nQT - 1; };
   auto next_head = [&](int g) {  // the first head from g on with a tile in range, or group
     while (g < group && qt_hi(g) < qt0) ++g;
@@ -657,7 +657,6 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   // Query tiles run from the last one down: the key blocks of a head that run together
   // then read the same Q / dO tiles at about the same time (shared through L2).
   int gi = next_head(0), qt = gi < group ? qt_hi(gi) : 0;  // current work item; the next one is (gn, qn)
-  __syncthreads();  // zeroed tiles before the first DMA lands
   if (nwork > 0) {
     issue_tile(gi, qt, 0);
     load_stats(gi, qt);
