@@ -24,6 +24,8 @@ EXPORTS = (
     "co_alibi_zb_numel",
     "co_alibi_bwd_workspace_bytes",
     "co_alibi_fwd",
+    "co_alibi_fwd_inference_workspace_bytes",
+    "co_alibi_fwd_inference",
     "co_alibi_bwd",
     "co_alibi_bwd_dq",
     "co_alibi_bwd_dkdv",
@@ -44,6 +46,8 @@ _SIGNATURES = {
     "co_alibi_zb_numel": (_Z, [_I, _I, _I, _I]),
     "co_alibi_bwd_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "co_alibi_fwd": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "co_alibi_fwd_inference_workspace_bytes": (_Z, [_I, _I, _I]),
+    "co_alibi_fwd_inference": (_I, [_I, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
     "co_alibi_bwd": (
         _I,
         [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _F, _P],
@@ -81,7 +85,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.co_alibi_abi_version() != 2:
+        if handle.co_alibi_abi_version() != 3:
             raise RuntimeError("co_alibi_attn: native library ABI version mismatch")
         _lib = handle
     return _lib

@@ -123,10 +123,21 @@ size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_k
   return round_up(rows * sizeof(float), 256) + zb_block_numel(batch, heads_q, seq_q, seq_kv) * sizeof(float);
 }
 
-int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const float* slopes, void* o,
-                 float* lse, float* zb, int batch, int heads_q, int heads_kv, int seq_q, int seq_kv,
-                 int head_dim, int causal, float sm_scale, void* stream) {
-  const char* fn = "co_alibi_fwd";
+size_t co_alibi_fwd_inference_workspace_bytes(int batch, int heads_q, int seq_kv) {
+  if (batch < 1 || heads_q < 1 || seq_kv < 1) return 0;
+  return round_up(static_cast<size_t>(batch) * heads_q * coalibi::zb_knorm_count(seq_kv) * sizeof(float), 256);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The forward with its statistics (lse, zb with the kstart / knorm tails), without them
+// (lse = zb = NULL: no tail skip), or for inference (knorm scratch only: the tail skip
+// without the backward's statistics).
+int fwd_impl(const char* fn, int dtype, const void* q, const void* k, const void* v, const float* slopes, void* o,
+             float* lse, float* zb, float* knorm_ws, int batch, int heads_q, int heads_kv, int seq_q, int seq_kv,
+             int head_dim, int causal, float sm_scale, void* stream) {
   const Shape s{batch, heads_q, heads_kv, seq_q, seq_kv, head_dim};
   int rc;
   if ((rc = check_shape(fn, dtype, s))) return rc;
@@ -134,7 +145,7 @@ int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const f
       (rc = check_ptr(fn, "o", o, 16)) || (rc = check_ptr(fn, "slopes", slopes, 4)) ||
       (rc = check_opt_ptr(fn, "lse", lse, 4)) || (rc = check_opt_ptr(fn, "zb", zb, 4)))
     return rc;
-  if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, "co_alibi_fwd: sm_scale must be finite");
+  if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": sm_scale must be finite");
 
   coalibi::FwdArgs a{};
   a.q = q;
@@ -148,6 +159,8 @@ int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const f
     float* tail = zb + zb_block_numel(batch, heads_q, seq_q, seq_kv);
     a.kstart = reinterpret_cast<int*>(tail);
     a.knorm = tail + static_cast<size_t>(batch) * heads_q * coalibi::zb_kstart_count(seq_q);
+  } else {
+    a.knorm = knorm_ws;
   }
   a.B = batch;
   a.Hq = heads_q;
@@ -164,8 +177,33 @@ int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const f
     case CO_ALIBI_BF16: e = fwd_dispatch_d<__bf16>(a, head_dim, causal != 0, st); break;
     default: e = fwd_dispatch_d<float>(a, head_dim, causal != 0, st); break;
   }
-  if (e != hipSuccess) return fail(CO_ALIBI_ELAUNCH, std::string("co_alibi_fwd: launch failed: ") + hipGetErrorString(e));
+  if (e != hipSuccess) return fail(CO_ALIBI_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
   return CO_ALIBI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const float* slopes, void* o,
+                 float* lse, float* zb, int batch, int heads_q, int heads_kv, int seq_q, int seq_kv,
+                 int head_dim, int causal, float sm_scale, void* stream) {
+  return fwd_impl("co_alibi_fwd", dtype, q, k, v, slopes, o, lse, zb, nullptr, batch, heads_q, heads_kv, seq_q,
+                  seq_kv, head_dim, causal, sm_scale, stream);
+}
+
+int co_alibi_fwd_inference(int dtype, const void* q, const void* k, const void* v, const float* slopes, void* o,
+                           void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv, int seq_q,
+                           int seq_kv, int head_dim, int causal, float sm_scale, void* stream) {
+  const char* fn = "co_alibi_fwd_inference";
+  int rc;
+  if ((rc = check_ptr(fn, "workspace", workspace, 256))) return rc;
+  const size_t need = co_alibi_fwd_inference_workspace_bytes(batch, heads_q, seq_kv);
+  if (workspace_bytes < need)
+    return fail(CO_ALIBI_EINVAL, std::string(fn) + ": workspace of " + std::to_string(workspace_bytes) +
+                                     " bytes, need " + std::to_string(need));
+  return fwd_impl(fn, dtype, q, k, v, slopes, o, nullptr, nullptr, static_cast<float*>(workspace), batch, heads_q,
+                  heads_kv, seq_q, seq_kv, head_dim, causal, sm_scale, stream);
 }
 
 }  // extern "C"
@@ -452,6 +490,6 @@ int co_alibi_decode_noalloc(int dtype, const void* q, const void* k_cache, const
 
 const char* co_alibi_last_error(void) { return g_last_error.c_str(); }
 
-int co_alibi_abi_version(void) { return 2; }
+int co_alibi_abi_version(void) { return 3; }
 
 }  // extern "C"

@@ -264,7 +264,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   __shared__ float sKmax[4];
   __shared__ float sBound[kFwdBM];
   __shared__ int sDone[4];
-  const bool tail_skip = args.kstart != nullptr && lam2 > 0.f;
+  const bool tail_skip = args.knorm != nullptr && lam2 > 0.f;
   if (tail_skip) {
     float qq = 0.f;
 #pragma unroll
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
   static_assert(kFwdBM == kSkipRows, "kstart entries are per forward row block");
-  if (a.kstart != nullptr) {
+  if (a.knorm != nullptr) {
     hipLaunchKernelGGL((coalibi_key_norm_kernel<T, D>), dim3(a.nKC * a.B * a.Hq), dim3(256), 0, stream,
                        static_cast<const T*>(a.k), const_cast<float*>(a.knorm), a.Skv, a.nKC, a.B * a.Hkv);
     const hipError_t e = hipGetLastError();

@@ -42,8 +42,8 @@ struct FwdArgs {
   void* o;
   float* lse;  // (B*Hq, Sq) natural-log log-sum-exp
   float* zb;
-  int* kstart;         // (B*Hq, nQB) or NULL (no tail skip: inference without statistics)
-  const float* knorm;  // (B*Hkv, nKC) chunk maxima of |k|, with kstart
+  int* kstart;         // (B*Hq, nQB), written when not NULL (the backward's statistics)
+  const float* knorm;  // (B*Hq, nKC) chunk maxima of |k|, filled before the forward; NULL: no tail skip
   int B, Hq, Hkv, Sq, Skv, nZB, nKC;
   float sc2;  // sm_scale * log2(e)
 };
@@ -99,7 +99,7 @@ struct DecodeArgs {
 // Split-K work-groups the decode aims at per CU: one round of the two that are resident.
 constexpr int kDecodeWGsPerCU = 2;
 
-// Forward; with a.kstart it first launches the key-norm kernel that fills a.knorm.
+// Forward; with a.knorm it first launches the key-norm kernel that fills it.
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 

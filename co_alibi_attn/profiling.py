@@ -111,9 +111,12 @@ class KernelSet:
                                                 p(self.zb), p(self.lam), p(self.dk), p(self.dv), p(self.ws),
                                                 self.ws_bytes, *shape))
 
-        def fwd_inference():  # no LSE / zb: the forward of a caller that needs no backward
-            _native.check(lib.co_alibi_fwd(code, p(self.q), p(self.k), p(self.v), p(self.lam), p(self.o), 0, 0,
-                                           *shape))
+        self.ws_inf_bytes = lib.co_alibi_fwd_inference_workspace_bytes(B, Hq, S)
+        self.ws_inf = torch.empty(self.ws_inf_bytes, device=dev, dtype=torch.uint8)
+
+        def fwd_inference():  # no LSE / zb: the forward of a caller that needs no backward (tail skip included)
+            _native.check(lib.co_alibi_fwd_inference(code, p(self.q), p(self.k), p(self.v), p(self.lam), p(self.o),
+                                                     p(self.ws_inf), self.ws_inf_bytes, *shape))
 
         self.launch = dict(zip(KERNELS, (fwd, dq, dkdv)))
         self.launch["coalibi_fwd_kernel (inference)"] = fwd_inference

@@ -68,6 +68,18 @@ int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const f
                  void* o, float* lse, float* zb, int batch, int heads_q, int heads_kv, int seq_q,
                  int seq_kv, int head_dim, int causal, float sm_scale, void* stream);
 
+/* Forward for inference with the tail skip: o only (no lse or zb), skipping the keys
+ * whose softmax weight is below 2^-64 of the row total as co_alibi_fwd does with its
+ * statistics (co_alibi_fwd with lse = zb = NULL computes every key).  workspace holds
+ * co_alibi_fwd_inference_workspace_bytes(...) bytes (256-byte aligned): the largest |k|
+ * per 256-key chunk of every key head.  No counterpart in the reference, whose forward
+ * always saves its statistics (co_alibi_attn.py:35-57). */
+size_t co_alibi_fwd_inference_workspace_bytes(int batch, int heads_q, int seq_kv);
+int co_alibi_fwd_inference(int dtype, const void* q, const void* k, const void* v, const float* slopes,
+                           void* o, void* workspace, size_t workspace_bytes, int batch, int heads_q,
+                           int heads_kv, int seq_q, int seq_kv, int head_dim, int causal, float sm_scale,
+                           void* stream);
+
 /* Backward: given dout and the forward's q, k, v, o, lse, zb, writes dq
  * (B,Hq,Sq,D), dk and dv (B,Hkv,Skv,D), all in dtype.  For Hkv < Hq the key /
  * value gradients are summed over the query heads of each group.  workspace
@@ -141,7 +153,7 @@ int co_alibi_probe_mfma(void* ticks, void* sink, int blocks, int iters, void* st
 /* Message describing the last failed call on this thread ("" if none). */
 const char* co_alibi_last_error(void);
 
-/* ABI version of this header: 2 (the zb buffer gained its kstart / knorm tails). */
+/* ABI version of this header: 3 (co_alibi_fwd_inference; the zb buffer has kstart / knorm tails). */
 int co_alibi_abi_version(void);
 
 #ifdef __cplusplus

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in co_alibi.h but not exported"
     assert sorted(_native.EXPORTS) == declared
-    assert lib.co_alibi_abi_version() == 2
+    assert lib.co_alibi_abi_version() == 3
 
 
 def test_sizes():
@@ -65,6 +65,22 @@ def test_fwd_argument_errors(over, code, msg):
     lib = _native.lib()
     assert _fwd(lib, **over) == code
     assert msg in lib.co_alibi_last_error().decode()
+
+
+def test_fwd_inference_workspace():
+    """co_alibi_fwd_inference: its scratch is the key-norm chunk maxima (B*Hq*ceil(Skv/256) floats,
+    256-byte rounded), and a smaller or misaligned workspace is rejected before any launch."""
+    lib = _native.lib()
+    assert lib.co_alibi_fwd_inference_workspace_bytes(4, 16, 4096) == 4 * 16 * 16 * 4
+    assert lib.co_alibi_fwd_inference_workspace_bytes(1, 3, 300) == 256
+    assert lib.co_alibi_fwd_inference_workspace_bytes(0, 3, 300) == 0
+    P = 256
+    rc = lib.co_alibi_fwd_inference(1, P, P, P, P, P, P, 0, 1, 2, 2, 8, 8, 64, 1, 0.125, None)
+    assert rc == 1 and "workspace of 0 bytes, need 256" in lib.co_alibi_last_error().decode()
+    rc = lib.co_alibi_fwd_inference(1, P, P, P, P, P, 16, 1 << 20, 1, 2, 2, 8, 8, 64, 1, 0.125, None)
+    assert rc == 1 and "workspace" in lib.co_alibi_last_error().decode()
+    rc = lib.co_alibi_fwd_inference(1, P, P, P, P, P, P, 1 << 20, 1, 2, 2, 8, 8, 48, 1, 0.125, None)
+    assert rc == 2 and "head_dim" in lib.co_alibi_last_error().decode()
 
 
 def test_bwd_argument_errors():

@@ -210,10 +210,13 @@ def test_repeat_call_deterministic():
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["fp16", "bf16", "fp32"])
 def test_inference_forward_equals_training_forward(dtype):
-    """Without gradients the forward writes no LSE / zb and returns bit-identical O
-    (drop-in API under no_grad, with inputs that need no grad, and the C ABI with NULL)."""
+    """Without gradients the forward writes no LSE / zb and returns bit-identical O (drop-in API
+    under no_grad, with inputs that need no grad: co_alibi_fwd_inference, whose tail skip takes
+    the same decisions as the training forward's).  co_alibi_fwd with NULL statistics skips
+    nothing: equal in fp16 (every skipped weight rounds to zero in P), within 1e-6 otherwise."""
     lib = _native.lib()
-    for B, Hq, Hkv, Sq, Skv, D, causal in [(1, 4, 2, 200, 200, 64, True), (1, 2, 2, 70, 190, 128, False)]:
+    for B, Hq, Hkv, Sq, Skv, D, causal in [(1, 4, 2, 200, 200, 64, True), (1, 2, 2, 70, 190, 128, False),
+                                           (1, 4, 2, 1200, 1200, 64, True)]:  # the last one skips
         q, k, v, _ = rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=9)
         qd, kd, vd = (t.to(DEV) for t in (q, k, v))
         o_train = co_alibi_attention(qd.clone().requires_grad_(), kd, vd, causal=causal)
@@ -224,12 +227,23 @@ def test_inference_forward_equals_training_forward(dtype):
         assert o_nograd.grad_fn is None and o_plain.grad_fn is None
         assert torch.equal(o_train.detach(), o_nograd) and torch.equal(o_nograd, o_plain)
         lam = ref.slopes(Hq, 8.0, dtype=dtype).float().to(DEV)  # the drop-in's slopes, kept alive
-        o_abi = torch.empty_like(qd)
+        st = torch.cuda.current_stream().cuda_stream
+        o_abi, o_inf = torch.empty_like(qd), torch.empty_like(qd)
         _native.check(lib.co_alibi_fwd(_native.DTYPE_CODES[dtype], qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
                                        lam.data_ptr(), o_abi.data_ptr(), 0, 0, B, Hq, Hkv, Sq, Skv, D,
-                                       int(causal), 1.0 / math.sqrt(D), torch.cuda.current_stream().cuda_stream))
+                                       int(causal), 1.0 / math.sqrt(D), st))
+        ws_bytes = lib.co_alibi_fwd_inference_workspace_bytes(B, Hq, Skv)
+        ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+        _native.check(lib.co_alibi_fwd_inference(_native.DTYPE_CODES[dtype], qd.data_ptr(), kd.data_ptr(),
+                                                 vd.data_ptr(), lam.data_ptr(), o_inf.data_ptr(), ws.data_ptr(),
+                                                 ws_bytes, B, Hq, Hkv, Sq, Skv, D, int(causal),
+                                                 1.0 / math.sqrt(D), st))
         torch.cuda.synchronize()
-        assert torch.equal(o_abi, o_plain)
+        assert torch.equal(o_inf, o_plain)
+        if dtype == torch.float16:
+            assert torch.equal(o_abi, o_plain)
+        else:
+            assert (o_abi.float() - o_plain.float()).abs().max().item() <= 1e-6
 
 
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
