@@ -309,7 +309,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   for (int kt = nkt - 1; kt >= kt_end; --kt) {
     __syncthreads();
     // Every wavefront's rows passed the tail test after tile kt + 1: the keys left of it
-    // carry weights below 2^-kSkipLog2 (the vote is uniform, so all wavefronts leave here).
+    // carry weights below 2^-skip_log2<T>() (the vote is uniform, so all wavefronts leave here).
     // Leaving through the loop bound rather than a break keeps the loop's register
     // allocation as it is without the skip (a break costs 13 spilled registers at D = 128).
     if (tail_skip && kt < nkt - 1 && (sDone[0] & sDone[1] & sDone[2] & sDone[3])) {
@@ -358,7 +358,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     }
     if (tail_skip) {
       // Every key left of k0 has z >= zr, so its weight is at most 2^(bound - lam2*zr - m2).
-      const bool done = !row_ok || (m2 != kNegInf && sBound[wave * 32 + col] - lam2 * zr - m2 < -kSkipLog2);
+      const bool done =
+          !row_ok || (m2 != kNegInf && sBound[wave * 32 + col] - lam2 * zr - m2 < -skip_log2<T>());
       const bool all = __all(done);
       if (lane == 0) sDone[wave] = all;
     }

@@ -15,7 +15,7 @@ constexpr float kLog2eHost = 1.4426950408889634f;
 // two small arrays:
 //   kstart (B*Hq, nQB) int32, nQB = ceil(Sq/128): the first key the forward processed
 //     for each 128-row block.  Every key left of it has a softmax weight below
-//     2^-kSkipLog2 of its row's total in every row of the block (the tail skip below);
+//     2^-skip_log2 of its row's total in every row of the block (the tail skip below);
 //     the backward passes skip the same keys, and zb of those blocks is not written;
 //   knorm (B*Hq, nKC) fp32, nKC = ceil(Skv/kNormKeys): max_k |k|_2 over each chunk of
 //     kNormKeys keys of key head b*Hkv + h in its first B*Hkv rows, zero in the rest.
@@ -26,11 +26,22 @@ constexpr float kLog2eHost = 1.4426950408889634f;
 // k_next on, z_k >= zr (the sum over those keys) for every k < k_next, as sigmoids are
 // >= 0, and |t_k| <= |q| * max|k| * sm_scale * log2(e) =: bound (Cauchy-Schwarz).  With
 // lam2 > 0 and m2 the running maximum, every later weight 2^(a_k - m2) is then at most
-// 2^(bound - lam2 * zr - m2); once that is below 2^-kSkipLog2 for all rows of a 128-row
+// 2^(bound - lam2 * zr - m2); once that is below 2^-skip_log2 for all rows of a 128-row
 // block the forward stops.  The row total l is >= 1 at the final scale, so each skipped
-// weight is below 2^-kSkipLog2 of it (the softmax probability s = 2^(a - LSE2) too).
+// weight is below 2^-skip_log2 of it (the softmax probability s = 2^(a - LSE2) too).
+// The threshold follows the type P is rounded to before it multiplies V:
+//   fp16: 26 -- P < 2^-26 rounds to zero (below half the smallest subnormal, 2^-25), so
+//     the forward's O is bit-identical to the unskipped one;
+//   bf16: 32 -- P keeps 8 bits, so each P carries a relative error up to 2^-9; the skipped
+//     weights together are below S * 2^-32 of the row total (1e-6 at S = 4096);
+//   fp32: 64 -- the validation mode stays within S * 2^-64 of the unskipped result.
+// The backward leaves out the same keys; their dA = s (dS - D) terms are below the same
+// fraction of the row's scale.
 constexpr int kNormKeys = 256;
-constexpr float kSkipLog2 = 64.0f;
+template <typename T>
+constexpr float skip_log2() {
+  return sizeof(T) == 4 ? 64.0f : (__is_same(T, __bf16) ? 32.0f : 26.0f);
+}
 constexpr int kSkipRows = 128;  // rows per kstart entry: the forward's and pass 1's row block
 inline int zb_kstart_count(int Sq) { return (Sq + kSkipRows - 1) / kSkipRows; }
 inline int zb_knorm_count(int Skv) { return (Skv + kNormKeys - 1) / kNormKeys; }
