@@ -249,8 +249,9 @@ def test_inference_forward_equals_training_forward(dtype):
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["fp16", "bf16", "fp32"])
 def test_tail_skip(dtype, causal):
-    """Slopes large enough that the forward stops early (keys whose weight is below 2^-64 of
-    their row's total are left out, and the backward passes leave out the same keys):
+    """Slopes large enough that the forward stops early (keys whose weight is below 2^-26 (fp16),
+    2^-32 (bf16) or 2^-64 (fp32) of their row's total are left out, and the backward passes
+    leave out the same keys):
     - the first processed key per 128-row block (the zb tail) is a multiple of 64, positive for
       the steep heads, zero for the flat one, and no later than the block's diagonal tile;
     - O equals the forward without statistics, which skips nothing (bit for bit in fp16,
