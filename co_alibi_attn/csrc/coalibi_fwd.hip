@@ -249,11 +249,41 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   // 16-bit types: Q pre-scaled by sm_scale*log2(e) (one rounding per element, far below the
   // input precision's effect on q.k), so the tile math takes the scale 1 and multiplies by nothing.
   constexpr bool kPreScaled = sizeof(T) == 2;
+  // The reads before the first tile go out together and share one round trip: the Q
+  // fragments, the first K / V tile and (tail skip) the key-norm chunk maxima.
+  // Q through a buffer resource over the block's valid rows: rows past Sq read as zero with no
+  // branch (a conditional load makes the compiler wait for each load before the next).
   vec8 qf[C::KS];
+  {
+    const __amdgpu_buffer_rsrc_t qrs = tile_rsrc(Qp + (size_t)q0 * D, min(Sq - q0, kFwdBM) * D);
+    const int qoffb = ((wave * 32 + col) * D + hh * 8) * (int)sizeof(T);
 #pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) {
-    qf[ks] = row_ok ? ld_vec8(Qp + (size_t)row * D + ks * 16 + hh * 8) : zero_vec8<T>();
-    if constexpr (kPreScaled) qf[ks] = scale_vec8<T>(qf[ks], sc2);
+    for (int ks = 0; ks < C::KS; ++ks) {
+      const int off = qoffb + ks * 16 * (int)sizeof(T);
+      if constexpr (sizeof(T) == 2) {
+        qf[ks] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, 0));
+      } else {  // 8 fp32 values: two 16-byte loads
+        struct { u32x4 lo, hi; } two{__builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, 0),
+                                     __builtin_amdgcn_raw_buffer_load_b128(qrs, off + 16, 0, 0)};
+        qf[ks] = __builtin_bit_cast(vec8, two);
+      }
+    }
+  }
+  const int last_key = CAUSAL ? min(q0 + kFwdBM - 1, Skv - 1) : Skv - 1;
+  const int nkt = last_key / kFwdBN + 1;
+  KTile kt_regs;
+  VTile vt_regs;
+  kt_regs.load(Kp, (nkt - 1) * kFwdBN, Skv, tid);
+  vt_regs.load(Vp, (nkt - 1) * kFwdBN, Skv, tid);
+  const bool tail_skip = args.knorm != nullptr && lam2 > 0.f;
+  float km = 0.f;
+  if (tail_skip) {
+    const float* kn = args.knorm + ((size_t)b * args.Hkv + hkv) * args.nKC;
+    for (int c = tid; c < args.nKC; c += 256) km = kn[c] != kn[c] ? kn[c] : fmaxf(km, kn[c]);
+  }
+  if constexpr (kPreScaled) {
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) qf[ks] = scale_vec8<T>(qf[ks], sc2);
   }
   const float tile_sc2 = kPreScaled ? 1.0f : sc2;
 
@@ -264,7 +294,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   __shared__ float sKmax[4];
   __shared__ float sBound[kFwdBM];
   __shared__ int sDone[4];
-  const bool tail_skip = args.knorm != nullptr && lam2 > 0.f;
   if (tail_skip) {
     float qq = 0.f;
 #pragma unroll
@@ -272,9 +301,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
 #pragma unroll
       for (int e = 0; e < 8; ++e) qq = fmaf((float)qf[ks][e], (float)qf[ks][e], qq);
     qq += other_half(qq);
-    const float* kn = args.knorm + ((size_t)b * args.Hkv + hkv) * args.nKC;
-    float km = 0.f;
-    for (int c = tid; c < args.nKC; c += 256) km = kn[c] != kn[c] ? kn[c] : fmaxf(km, kn[c]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
       const float o = __shfl_xor(km, off);
@@ -288,14 +314,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     if (hh == 0) sBound[wave * 32 + col] = sqrtf(qq) * km * (kPreScaled ? 1.0f : sc2) * 1.001f + 1e-3f;
   }
   int kfirst = 0;  // first key of the leftmost tile processed
-
-  const int last_key = CAUSAL ? min(q0 + kFwdBM - 1, Skv - 1) : Skv - 1;
-  const int nkt = last_key / kFwdBN + 1;
-
-  KTile kt_regs;
-  VTile vt_regs;
-  kt_regs.load(Kp, (nkt - 1) * kFwdBN, Skv, tid);
-  vt_regs.load(Vp, (nkt - 1) * kFwdBN, Skv, tid);
 
   f32x16 acc[C::DT];
 #pragma unroll

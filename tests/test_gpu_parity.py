@@ -298,6 +298,39 @@ def test_tail_skip(dtype, causal):
                   f"tail skip causal={causal}", dtype)
 
 
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_tail_skip_grouped_rectangular(dtype, causal):
+    """The tail skip with grouped query heads of mixed steepness (the key head's pass-2 work list
+    mixes heads whose skipped ranges differ), Sq != Skv (top-left causal), two batches and
+    D = 128: forward and backward against the oracle."""
+    lib = _native.lib()
+    B, Hq, Hkv, Sq, Skv, D = 2, 6, 3, 700, 1100, 128
+    q, k, v, do = rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=23)
+    do = (do.float() * 0.5).to(dtype)
+    lam = torch.tensor([3.0, 0.02, 1.0, 0.5, 0.002, 2.0]).to(dtype).float()
+    scale = 1.0 / math.sqrt(D)
+    print(f"tail skip grouped {dtype} causal={causal}", flush=True)
+    qd, kd, vd, dod, lamd = (t.to(DEV) for t in (q, k, v, do, lam))
+    o, lse, zb = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
+    st = torch.cuda.current_stream().cuda_stream
+    ws_bytes = lib.co_alibi_bwd_workspace_bytes(B, Hq, Sq, Skv)
+    ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    _native.check(lib.co_alibi_bwd(_native.DTYPE_CODES[dtype], dod.data_ptr(), qd.data_ptr(), kd.data_ptr(),
+                                   vd.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), lamd.data_ptr(),
+                                   dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq, Hkv,
+                                   Sq, Skv, D, int(causal), scale, st))
+    torch.cuda.synchronize()
+    nzb, nqb = (Skv + 31) // 32, (Sq + 127) // 128
+    kstart = zb[B * Hq * nzb * Sq:B * Hq * (nzb * Sq + nqb)].view(torch.int32).view(B, Hq, nqb).cpu()
+    assert (kstart[:, 0].max() > 0) and (kstart[:, 4] == 0).all()  # the steep head skips, the flattest does not
+    ro, _ = ref.forward(q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
+    rdq, rdk, rdv = ref.backward(do.float(), q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
+    assert_parity(tuple(t.float().cpu() for t in (o, dq, dk, dv)), (ro, rdq, rdk, rdv), TOL[dtype],
+                  f"tail skip grouped causal={causal}", dtype)
+
+
 def test_sm_scale_and_bias_max_arguments():
     q, k, v, do = rand_inputs(1, 3, 3, 120, 120, 64, torch.float32, seed=5)
     got = hip_fwd_bwd(q, k, v, do, causal=True, sm_scale=0.3, bias_max=4.0)
