@@ -169,39 +169,58 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const int row = wrow0 + col;
   const bool row_ok = row < Sq;
 
-  vec8 qf[C::KS], dof[C::KS];
-  float dpart = 0.f;
   const float tile_sc2 = sizeof(T) == 2 ? 1.0f : args.sc2;  // Q carries the scale in 16-bit types
-  {
-    const T* __restrict__ Qr = static_cast<const T*>(args.q) + qoff + (size_t)row * D;
-    const T* __restrict__ dOr = static_cast<const T*>(args.dout) + qoff + (size_t)row * D;
-    const T* __restrict__ Or = static_cast<const T*>(args.o) + qoff + (size_t)row * D;
-#pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-      const int c0 = ks * 16 + hh * 8;
-      qf[ks] = row_ok ? ld_vec8(Qr + c0) : zero_vec8<T>();
-      // 16-bit types: Q pre-scaled by sm_scale*log2(e), as in the forward.
-      if constexpr (sizeof(T) == 2) qf[ks] = scale_vec8<T>(qf[ks], args.sc2);
-      dof[ks] = row_ok ? ld_vec8(dOr + c0) : zero_vec8<T>();
-      const vec8 of = row_ok ? ld_vec8(Or + c0) : zero_vec8<T>();
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dpart += (float)dof[ks][e] * (float)of[e];
-    }
-  }
-  const float dsum = dpart + other_half(dpart);
-  const float lse2 = row_ok ? args.lse[(size_t)bh * Sq + row] * kLog2e : 0.f;
-  if (hh == 0 && row_ok) args.dsum[(size_t)bh * Sq + row] = dsum;
-
   const int last_key = CAUSAL ? min(q0 + kBM - 1, Skv - 1) : Skv - 1;
   const int nkt = last_key / kBN + 1;
   // Keys left of the forward's first processed key are skipped (their dA and dP are below
-  // 2^-64 of the row's scale, coalibi_kernels.h); the prefix C starts at zero there.
+  // 2^-T of the row's scale, coalibi_kernels.h); the prefix C starts at zero there.
   static_assert(kBM == kSkipRows, "kstart entries are per pass-1 row block");
   const int kt0 = args.kstart[(size_t)bh * nQB + qb] / kBN;
 
+  // The reads before the first tile go out together and share one round trip: the Q / dO / O
+  // fragments and the lse through buffer resources over the block's valid rows (rows past Sq
+  // read as zero), then the first K / V tile (its address waits only for kstart).
+  vec8 qf[C::KS], dof[C::KS], of[C::KS];
+  float lse2;
+  {
+    const int rows = min(Sq - q0, kBM);
+    const size_t blk = qoff + (size_t)q0 * D;
+    const __amdgpu_buffer_rsrc_t qrs = tile_rsrc(static_cast<const T*>(args.q) + blk, rows * D);
+    const __amdgpu_buffer_rsrc_t dors = tile_rsrc(static_cast<const T*>(args.dout) + blk, rows * D);
+    const __amdgpu_buffer_rsrc_t ors = tile_rsrc(static_cast<const T*>(args.o) + blk, rows * D);
+    const int offb = ((wave * 32 + col) * D + hh * 8) * (int)sizeof(T);
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
+      const int off = offb + ks * 16 * (int)sizeof(T);
+      qf[ks] = buffer_load_vec8<vec8>(qrs, off);
+      dof[ks] = buffer_load_vec8<vec8>(dors, off);
+      of[ks] = buffer_load_vec8<vec8>(ors, off);
+    }
+    const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(args.lse + (size_t)bh * Sq + q0, rows);
+    lse2 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (wave * 32 + col) * 4, 0, 0)) * kLog2e;
+  }
+  float dpart = 0.f;
+  // fp32 folds dO.O before the tile loads: holding O across them spills.
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dpart += dof[ks][e] * of[ks][e];
+  }
   Tile kregs, vregs;
   kregs.load(Kp, kt0 * kBN, Skv, tid);
   vregs.load(Vp, kt0 * kBN, Skv, tid);
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
+      // Q pre-scaled by sm_scale*log2(e), as in the forward.
+      qf[ks] = scale_vec8<T>(qf[ks], args.sc2);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dpart += (float)dof[ks][e] * (float)of[ks][e];
+    }
+  }
+  const float dsum = dpart + other_half(dpart);
+  if (hh == 0 && row_ok) args.dsum[(size_t)bh * Sq + row] = dsum;
 
   f32x16 acc[C::DT];
 #pragma unroll

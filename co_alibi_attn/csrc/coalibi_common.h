@@ -102,6 +102,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const T* p, int elem
   return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, bytes, kBufferRsrcWord3);
 }
 
+// Eight consecutive elements at byte offset `off` of a buffer resource (zero past its end):
+// one 16-byte load for 16-bit types, two for fp32.  No branch, so a run of these loads goes
+// out back to back (a conditional load makes the compiler wait for each one before the next).
+template <typename V>
+__device__ __forceinline__ V buffer_load_vec8(__amdgpu_buffer_rsrc_t r, int off) {
+  if constexpr (sizeof(V) == 16) {
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  } else {
+    static_assert(sizeof(V) == 32, "eight 2- or 4-byte elements");
+    struct { u32x4 lo, hi; } two{__builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0),
+                                 __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0)};
+    return __builtin_bit_cast(V, two);
+  }
+}
+
 // 16-byte buffer-to-LDS DMA: lane i of the wavefront writes the 16 bytes at byte offset
 // `voffset` of the resource to LDS address lds + 16*i (offsets past the resource read as
 // zero).  `lds` must be wave-uniform.  A plain function: inside kernel templates the

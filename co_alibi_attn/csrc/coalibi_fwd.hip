@@ -251,23 +251,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   constexpr bool kPreScaled = sizeof(T) == 2;
   // The reads before the first tile go out together and share one round trip: the Q
   // fragments, the first K / V tile and (tail skip) the key-norm chunk maxima.
-  // Q through a buffer resource over the block's valid rows: rows past Sq read as zero with no
-  // branch (a conditional load makes the compiler wait for each load before the next).
+  // Q through a buffer resource over the block's valid rows: rows past Sq read as zero.
   vec8 qf[C::KS];
   {
     const __amdgpu_buffer_rsrc_t qrs = tile_rsrc(Qp + (size_t)q0 * D, min(Sq - q0, kFwdBM) * D);
     const int qoffb = ((wave * 32 + col) * D + hh * 8) * (int)sizeof(T);
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-      const int off = qoffb + ks * 16 * (int)sizeof(T);
-      if constexpr (sizeof(T) == 2) {
-        qf[ks] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, 0));
-      } else {  // 8 fp32 values: two 16-byte loads
-        struct { u32x4 lo, hi; } two{__builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, 0),
-                                     __builtin_amdgcn_raw_buffer_load_b128(qrs, off + 16, 0, 0)};
-        qf[ks] = __builtin_bit_cast(vec8, two);
-      }
-    }
+    for (int ks = 0; ks < C::KS; ++ks) qf[ks] = buffer_load_vec8<vec8>(qrs, qoffb + ks * 16 * (int)sizeof(T));
   }
   const int last_key = CAUSAL ? min(q0 + kFwdBM - 1, Skv - 1) : Skv - 1;
   const int nkt = last_key / kFwdBN + 1;
