@@ -266,7 +266,7 @@ def main():
     print(f"[bench] {args.steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f} s)", file=sys.stderr, flush=True)
 
     # Per-kernel timing through the C ABI, HIP events on the launch stream.
-    from co_alibi_attn.profiling import KERNELS, KernelSet, read_traffic
+    from co_alibi_attn.profiling import KernelSet, read_traffic
 
     B, Hq, Hkv, S, D = w.batch, w.heads_q, w.heads_kv, w.seq, w.head_dim
     ks = KernelSet(w, dev)
@@ -274,13 +274,13 @@ def main():
     torch.cuda.synchronize()
     # Rounds of every kernel in turn, median per kernel: the first launches after the step loop
     # run slower (clock and cache state), and interleaving keeps the kernels comparable.
-    timed = {name: [] for name in (*KERNELS, "coalibi_fwd_kernel (inference)")}
+    timed = {name: [] for name in (*ks.kernels, "coalibi_fwd_kernel (inference)")}
     for _ in range(args.kernel_rounds):
         for name in timed:
             timed[name].append(ks.time(name, args.kernel_reps))
     med = {name: sorted(v)[len(v) // 2] for name, v in timed.items()}
     per_kernel = {}
-    for name in KERNELS:
+    for name in ks.kernels:
         ms = med[name]
         per_kernel[name] = {"ms": round(ms, 4),
                             "tflops": round(ks.charged_flops(name) / (ms * 1e-3) / 1e12, 2),
@@ -288,7 +288,7 @@ def main():
                             "issued_gflop": round(ks.issued_flops(name) / 1e9, 2)}
     fwd_inference_ms = med["coalibi_fwd_kernel (inference)"]
     fwd_ms = per_kernel["coalibi_fwd_kernel"]["ms"]
-    bwd_ms = per_kernel["coalibi_bwd_dq_kernel"]["ms"] + per_kernel["coalibi_bwd_dkdv_kernel"]["ms"]
+    bwd_ms = per_kernel[ks.kernels[1]]["ms"] + per_kernel[ks.kernels[2]]["ms"]
     dominant = max(per_kernel, key=lambda n: per_kernel[n]["ms"])
     peak = MFMA_PEAK_TFLOPS[dtype_name]
     achieved = per_kernel[dominant]["tflops"]

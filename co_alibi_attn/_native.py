@@ -23,6 +23,7 @@ DECODE_SCRATCH_BYTES = 32 << 20
 EXPORTS = (
     "co_alibi_zb_numel",
     "co_alibi_bwd_workspace_bytes",
+    "co_alibi_bwd_score_store_workspace_bytes",
     "co_alibi_fwd",
     "co_alibi_fwd_inference_workspace_bytes",
     "co_alibi_fwd_inference",
@@ -45,6 +46,7 @@ _Z = ctypes.c_size_t
 _SIGNATURES = {
     "co_alibi_zb_numel": (_Z, [_I, _I, _I, _I]),
     "co_alibi_bwd_workspace_bytes": (_Z, [_I, _I, _I, _I]),
+    "co_alibi_bwd_score_store_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I, _I]),
     "co_alibi_fwd": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
     "co_alibi_fwd_inference_workspace_bytes": (_Z, [_I, _I, _I]),
     "co_alibi_fwd_inference": (_I, [_I, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
@@ -81,12 +83,16 @@ def lib() -> ctypes.CDLL:
                 "run `python -m co_alibi_attn._build`"
             )
         handle = ctypes.CDLL(LIB_PATH)
+        # The version first: a library of another ABI may lack some of the symbols below.
+        handle.co_alibi_abi_version.restype = ctypes.c_int
+        handle.co_alibi_abi_version.argtypes = []
+        if handle.co_alibi_abi_version() != 4:
+            raise RuntimeError("co_alibi_attn: native library ABI version mismatch; "
+                               "run `python -m co_alibi_attn._build`")
         for name, (res, args) in _SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.co_alibi_abi_version() != 3:
-            raise RuntimeError("co_alibi_attn: native library ABI version mismatch")
         _lib = handle
     return _lib
 

@@ -132,17 +132,22 @@ __device__ __forceinline__ void dp_tile(const f32x16& sacc, f32x16& dacc, float 
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1: dQ, D, cb.  Per wavefront 32 query rows; register r of lane (col, hh)
-// <-> key k0 + hh*16 + r.
-template <typename T, int D, bool CAUSAL>
+// Pass 1: dQ, D, and cb (recompute path) or the score store (STORE).  Per wavefront 32
+// query rows; register r of lane (col, hh) <-> key k0 + hh*16 + r.
+template <typename T, int D, bool CAUSAL, bool STORE>
 __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coalibi_bwd_dq_kernel(BwdArgs args) {
   using C = BwdCfg<T, D>;
   using M = Mfma<T>;
   using vec8 = typename M::vec8;
   using Tile = TileLoader<T, D, kBN, !BwdCfg<T, D>::kTr>;
+  static_assert(!STORE || C::kTr, "the score store holds 16-bit operands");
   __shared__ __align__(16) T sK[kBN * C::LDR];
   __shared__ __align__(16) T sV[kBN * C::LDR];
   __shared__ __align__(16) T sKt[C::kTr ? 8 : C::DP * C::LDT1];
+  // STORE: per wavefront, s and dS of its 32 x 32 tile as [row][key], to be read back in
+  // operand order.
+  constexpr int kScLD = 32 + C::CH;
+  __shared__ __align__(16) T sSc[STORE ? 4 * 2 * 32 * kScLD : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, hh = lane >> 5;
@@ -227,7 +232,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
   float crun = 0.f;
   const float* __restrict__ zb_row = args.zb + (size_t)bh * args.nZB * Sq + row;
-  float* __restrict__ cb_row = args.cb + (size_t)bh * args.nZB * Sq + row;
+  float* __restrict__ cb_row = STORE ? nullptr : args.cb + (size_t)bh * args.nZB * Sq + row;
+  const int nQ32 = (Sq + 31) / 32;
 
   for (int kt = kt0; kt < nkt; ++kt) {
     __syncthreads();
@@ -245,8 +251,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     const bool masked = (CAUSAL && k0 + kBN - 1 > wrow0) || (k0 + kBN > Skv) || (wrow0 + 32 > Sq);
 
     f32x16 sacc = f32x16{}, dacc;
+    // The 16-register start value of the dS accumulator is rebuilt every tile (16 moves):
+    // hoisted out of the loop it would hold 16 registers for the whole kernel.
+    float ndsum = -dsum;
+    asm volatile("" : "+v"(ndsum));
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dacc[r] = -dsum;
+    for (int r = 0; r < 16; ++r) dacc[r] = ndsum;
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
       sacc = M::k16(ld_vec8(sK + col * C::LDR + ks * 16 + hh * 8), qf[ks], sacc);
@@ -261,7 +271,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     else
       dp_tile<T, false, CAUSAL>(sacc, dacc, zb, crun, lse2, k0 + hh * 16, row, hh, Skv, Sq, tile_sc2, lam, lam2,
                                 sb, pb, atot);
-    if (hh == 0 && row_ok) cb_row[(size_t)kt * Sq] = crun;
+    if constexpr (!STORE) {
+      if (hh == 0 && row_ok) cb_row[(size_t)kt * Sq] = crun;
+    }
     crun += atot;
     __builtin_amdgcn_sched_barrier(0);
     // dQ^T[d][q] += K^T[d][key] dP^T[key][q];  A rows are keys hh*16 + mh*8 + e.
@@ -275,6 +287,30 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
         else
           ka = ld_vec8(sKt + (dt * 32 + col) * C::LDT1 + hh * 16 + mh * 8);
         acc[dt] = M::k16(ka, pb[mh], acc[dt]);
+      }
+    }
+    // Score store: after the dQ products, the tile's s and dS go through this wavefront's
+    // LDS scratch ([row][key]) and back out in the operand order of pass 2, one 16-byte store
+    // per lane and operand (a record is 4 KB written by one wavefront).  Rows past Sq have
+    // no record.
+    if constexpr (STORE) {
+      if (wrow0 < Sq) {
+        T* __restrict__ sc = sSc + wave * 2 * 32 * kScLD;
+        *reinterpret_cast<vec8*>(sc + col * kScLD + hh * 16) = sb[0];
+        *reinterpret_cast<vec8*>(sc + col * kScLD + hh * 16 + 8) = sb[1];
+        *reinterpret_cast<vec8*>(sc + (32 + col) * kScLD + hh * 16) = pb[0];
+        *reinterpret_cast<vec8*>(sc + (32 + col) * kScLD + hh * 16 + 8) = pb[1];
+        // The transpose reads take other lanes' values: keep the compiler from moving them
+        // above the writes (LDS operations of one wavefront execute in order).
+        asm volatile("" ::: "memory");
+        u32x4* rec = reinterpret_cast<u32x4*>(static_cast<char*>(args.scores) +
+                                              ((size_t)bh * args.score_head + score_record(kt, wrow0 / 32, nQ32, CAUSAL)) *
+                                                  kScoreRecordBytes) +
+                     lane;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          rec[m * 64] =
+              __builtin_bit_cast(u32x4, ld_kmajor<T, false>(sc + (m >> 1) * 32 * kScLD, kScLD, (m & 1) * 16, 8, 0, lane));
       }
     }
   }
@@ -531,6 +567,52 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
 // whose barriers do not align their phases) at no extra elementwise work.  The
 // next Q and dO tiles arrive by buffer-to-LDS DMA issued once the current tile is
 // no longer read; the other work-group on the CU covers that latency.
+// Pass 2's work list for one block of keys of a key head: (query head gi, query tile qt)
+// pairs, qt from qt_hi(gi) down to qt0 (the first tile that can see the block).  Tail skip:
+// kstart, the first key the forward processed for a 128-row block, is a multiple of 64, so
+// for every 64-row tile a 64-key block is processed or skipped as a whole.  qt_hi(gi) is the
+// last tile of head gi whose row block processed the keys (found once, in LDS, for up to
+// kMaxPairGroup query heads per key head; all tiles otherwise); a tile inside the range whose
+// row block skipped them is left out by the caller's own kstart test.
+constexpr int kMaxPairGroup = 64;
+struct KeyBlockWork {
+  int group, nQT, qt0;
+  bool ranged;
+  const int* qthi;  // LDS, one entry per query head of the group
+  __device__ __forceinline__ int qt_hi(int g) const { return ranged ? qthi[g] : nQT - 1; }
+  // the first head from g on with a tile in range, or group
+  __device__ __forceinline__ int next_head(int g) const {
+    while (g < group && qt_hi(g) < qt0) ++g;
+    return g;
+  }
+  __device__ __forceinline__ int count() const {
+    int n = 0;
+    for (int g = 0; g < group; ++g) n += max(qt_hi(g) - qt0 + 1, 0);
+    return n;
+  }
+};
+// Fills qthi for a key block starting at key kwg0 (wavefront w: heads w, w + nwaves, ...);
+// the caller synchronises before reading it.  BQ rows per tile, two tiles per kstart entry.
+template <int BQ>
+__device__ __forceinline__ KeyBlockWork key_block_work(int* qthi, const int* __restrict__ kstart_g, int group,
+                                                       int Sq, int qt0, int kwg0, int wave, int nwaves, int lane) {
+  static_assert(BQ * 2 == kSkipRows, "two query tiles per kstart row block");
+  const int nQT = (Sq + BQ - 1) / BQ;
+  const int nSkipQB = (Sq + kSkipRows - 1) / kSkipRows;
+  const bool ranged = group <= kMaxPairGroup;
+  if (ranged) {
+    for (int g = wave; g < group; g += nwaves) {
+      int hi = qt0 - 1;
+      for (int rb = lane; rb < nSkipQB; rb += 64)
+        if (kstart_g[(size_t)g * nSkipQB + rb] <= kwg0) hi = max(hi, min(2 * rb + 1, nQT - 1));
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) hi = max(hi, __shfl_xor(hi, off));
+      if (lane == 0) qthi[g] = hi;
+    }
+  }
+  return {group, nQT, qt0, ranged, qthi};
+}
+
 constexpr int kPairBK = 64;     // keys per work-group
 constexpr int kPairBQ = 64;     // query rows per tile
 constexpr int kPairWaves = 4;   // wavefronts per work-group: 2 key groups x 2 query halves
@@ -607,43 +689,23 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   static_assert(Dma::LDS_ELEMS == TILE, "every DMA writes its whole tile (pad and tail chunks as zero)");
   dma.init(wave, lane);
 
-  // Work list: (query head gi, query tile qt) pairs, qt from qt_hi(gi) down to qt0.
-  // Tail skip: kstart, the first key the forward processed for a 128-row block, is a
-  // multiple of 64, so for every tile this block's 64 keys are processed or skipped as a
-  // whole.  qt_hi(gi) is the last tile of head gi whose row block processed them (found
-  // once, in LDS, for up to kMaxPairGroup query heads per key head; all tiles otherwise),
-  // and a tile inside the range whose row block skipped them is left out by half_live.
-  static_assert(BQ * 2 == kSkipRows, "two query tiles per kstart row block");
-  constexpr int kMaxPairGroup = 64;
+  // Work list (key_block_work): (query head gi, query tile qt) pairs.
   __shared__ int sQtHi[kMaxPairGroup];
   const int nQT = (Sq + BQ - 1) / BQ;
   const int qt0 = CAUSAL ? min((kb * kPairBK) / BQ, nQT) : 0;
   const int nSkipQB = (Sq + kSkipRows - 1) / kSkipRows;
   const int kwg0 = kb * kPairBK;
   const int* __restrict__ kstart_g = args.kstart + (size_t)(b * args.Hq + hkv * group) * nSkipQB;
-  const bool ranged = group <= kMaxPairGroup;
-  if (ranged) {  // wavefront w finds qt_hi of heads w, w + kPairWaves, ...
-    for (int g = wave; g < group; g += kPairWaves) {
-      int hi = qt0 - 1;
-      for (int rb = lane; rb < nSkipQB; rb += 64)
-        if (kstart_g[(size_t)g * nSkipQB + rb] <= kwg0) hi = max(hi, min(2 * rb + 1, nQT - 1));
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) hi = max(hi, __shfl_xor(hi, off));
-      if (lane == 0) sQtHi[g] = hi;
-    }
-  }
+  const KeyBlockWork work =
+      key_block_work<BQ>(sQtHi, kstart_g, group, Sq, qt0, kwg0, wave, kPairWaves, lane);
   // K pre-scaled by sm_scale*log2(e), so S^T comes out in log2 units.
 #pragma unroll
   for (int ks = 0; ks < C::KS; ++ks) ka[ks] = scale_vec8<T>(ka[ks], args.sc2);
   __builtin_amdgcn_s_waitcnt(0);  // this wavefront's V DMA
   __syncthreads();                // the V tile and sQtHi
-  auto qt_hi = [&](int g) { return ranged ? sQtHi[g] : nQT - 1; };
-  auto next_head = [&](int g) {  // the first head from g on with a tile in range, or group
-    while (g < group && qt_hi(g) < qt0) ++g;
-    return g;
-  };
-  int nwork = 0;
-  for (int g = 0; g < group; ++g) nwork += max(qt_hi(g) - qt0 + 1, 0);
+  auto qt_hi = [&](int g) { return work.qt_hi(g); };
+  auto next_head = [&](int g) { return work.next_head(g); };
+  const int nwork = work.count();
   const int jb = kw0 / 32;  // this key group's 32-key block
   auto issue_tile = [&](int gi, int qt, int buf) {
     const size_t qoff = (size_t)(b * args.Hq + hkv * group + gi) * Sq * D;
@@ -784,18 +846,219 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   }
 }
 
+// Pass 2 from the score store (16-bit types, D = 64 or 128): dK and dV of 64 keys per
+// work-group, reduced from the s and dS records pass 1 wrote; nothing is recomputed.
+//   dV^T[d][key] += dO^T[d][q] s[q][key],  dK^T[d][key] += Q^T[d][q] dS[q][key].
+// Wavefront (kg, qh) accumulates key group kg (32 keys) over query half qh of every 64-row
+// tile, for the whole head dim; at the end the two halves are added through LDS.  The
+// B operands come from the records straight into registers (they are stored in MFMA lane
+// order), one tile ahead; the A operands are transpose reads of the Q and dO tiles, which
+// arrive by untracked buffer-to-LDS DMA into two buffers, one tile ahead.  One barrier per
+// tile: it publishes tile w and frees the buffer of tile w - 1 for tile w + 1.
+constexpr int kStoreBK = 64;  // keys per work-group
+constexpr int kStoreBQ = 64;  // query rows per tile
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs args) {
+  static_assert(sizeof(T) == 2 && (D == 64 || D == 128), "the score store path is 16-bit, D 64 or 128");
+  using C = BwdCfg<T, D>;
+  using M = Mfma<T>;
+  using vec8 = typename M::vec8;
+  constexpr int BQ = kStoreBQ;
+  constexpr int TILE = BQ * C::LDR;
+  using Dma = DmaTile<T, D, BQ, C::LDR, 4, false>;
+  static_assert(Dma::LDS_ELEMS == TILE, "every DMA writes its whole tile (pad and tail chunks as zero)");
+  __shared__ __align__(16) T sQ[2][TILE];
+  __shared__ __align__(16) T sdO[2][TILE];
+  __shared__ int sQtHi[kMaxPairGroup];
+  // Whether the forward processed this key block for row block rb of query head g: bit rb % 32
+  // of word g * wph + rb / 32 (kstart copied once, before any untracked DMA: loads after those
+  // cannot be proven unclobbered and would go through the vector memory counter, whose waits
+  // would also wait for the DMA).
+  __shared__ unsigned sProc[kStoreProcessedWords];
+  // The end-of-block exchange: 2 key groups x DT*16 accumulators x 64 lanes per half.
+  static_assert(2 * C::DT * 16 * 64 * sizeof(float) <= sizeof(sQ), "the exchange fits one tile pair");
+
+  // wave is uniform; readfirstlane lets the DMA slot choice stay scalar.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, hh = lane >> 5;
+  const int kg = wave >> 1, qh = wave & 1;
+  const int Sq = args.Sq, Skv = args.Skv;
+  static_assert(sizeof(sQ[1]) >= 2 * kMaxBalancedHeads * 4, "the head order is built in sQ[1]");
+  const WorkItem item = balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
+                                      reinterpret_cast<float*>(sQ[1]),
+                                      reinterpret_cast<int*>(sQ[1]) + kMaxBalancedHeads, tid, 256);
+  const int bhk = item.head;  // b * Hkv + hkv
+  const int kb = item.rank;   // rank 0: key block 0, seen by the most query rows
+  const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;
+  const int group = args.Hq / args.Hkv;
+  const size_t kvoff = (size_t)bhk * Skv * D;
+  const int kwg0 = kb * kStoreBK;
+  const int kw0 = kwg0 + kg * 32;  // first key of this wavefront's key group
+  const int jb = kw0 / 32;
+  const bool keys_ok = kw0 < Skv;
+
+  const int nQT = (Sq + BQ - 1) / BQ;
+  const int qt0 = CAUSAL ? min(kwg0 / BQ, nQT) : 0;
+  const int nSkipQB = (Sq + kSkipRows - 1) / kSkipRows;
+  const int* __restrict__ kstart_g = args.kstart + (size_t)(b * args.Hq + hkv * group) * nSkipQB;
+  const KeyBlockWork work = key_block_work<BQ>(sQtHi, kstart_g, group, Sq, qt0, kwg0, wave, 4, lane);
+  const int wph = (nSkipQB + 63) / 64 * 2;  // words per head (the host checks group * wph fits)
+  for (int g = wave; g < group; g += 4) {
+    for (int rb0 = 0; rb0 < nSkipQB; rb0 += 64) {
+      const int rb = rb0 + lane;
+      const unsigned long long m = __ballot(rb < nSkipQB && kstart_g[(size_t)g * nSkipQB + rb] <= kwg0);
+      if (lane == 0) {
+        sProc[g * wph + rb0 / 32] = static_cast<unsigned>(m);
+        sProc[g * wph + rb0 / 32 + 1] = static_cast<unsigned>(m >> 32);
+      }
+    }
+  }
+  __syncthreads();  // sQtHi, sProc; the head-order scratch in sQ[1] is free again
+  const int nwork = work.count();
+  const int nQ32 = (Sq + 31) / 32;
+
+  Dma dma;
+  dma.init(wave, lane);
+  auto issue_tile = [&](int gi, int qt, int buf) {
+    const size_t qoff = (size_t)(b * args.Hq + hkv * group + gi) * Sq * D;
+    dma.issue_untracked(static_cast<const T*>(args.q) + qoff, qt * BQ, Sq, sQ[buf], wave);
+    dma.issue_untracked(static_cast<const T*>(args.dout) + qoff, qt * BQ, Sq, sdO[buf], wave);
+  };
+  // This wavefront's query half of tile qt holds visible pairs of its key group that the
+  // forward processed: exactly the records pass 1 wrote.
+  auto live = [&](int gi, int qt) {
+    const int qs0 = qt * BQ + qh * 32;
+    const int rb = qt / 2;
+    return ((sProc[gi * wph + rb / 32] >> (rb % 32)) & 1u) != 0 && keys_ok && qs0 < Sq &&
+           (!CAUSAL || qs0 + 31 >= kw0);
+  };
+  // The four operands of the record, 16 bytes per lane each; a record that is not live is
+  // read through an empty resource (zeros, and no branch around the loads).
+  auto load_record = [&](int gi, int qt, vec8 (&r)[4]) {
+    const bool ok = live(gi, qt);
+    const size_t bh = (size_t)b * args.Hq + hkv * group + gi;
+    const int qb = qt * 2 + qh;
+    const char* base = static_cast<const char*>(args.scores) +
+                       (ok ? (bh * args.score_head + score_record(jb, qb, nQ32, CAUSAL)) * kScoreRecordBytes : 0);
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(reinterpret_cast<const u32x4*>(base), ok ? kScoreRecordBytes / 16 : 0);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) r[m] = buffer_load_vec8<vec8>(rs, (m * 64 + lane) * 16);
+  };
+
+  f32x16 dk[C::DT], dv[C::DT];
+#pragma unroll
+  for (int i = 0; i < C::DT; ++i) {
+    dk[i] = f32x16{};
+    dv[i] = f32x16{};
+  }
+  vec8 ra[4], rb[4];
+  int gi = work.next_head(0), qt = gi < group ? work.qt_hi(gi) : 0;  // current item
+  int gn = gi, qn = qt;                                                // next item
+  auto advance = [&]() {
+    const bool wrap = qn == qt0;
+    const int g2 = wrap ? work.next_head(gn + 1) : gn;
+    qn = wrap ? (g2 < group ? work.qt_hi(g2) : 0) : qn - 1;
+    gn = g2;
+  };
+  if (nwork > 0) {
+    issue_tile(gi, qt, 0);
+    load_record(gi, qt, ra);
+    advance();
+  }
+  // Tile w: its Q / dO in buffer w & 1, its record in `cur`; the next item (gn, qn) is
+  // fetched into the other buffer and `nxt`.
+  auto step = [&](int w, vec8 (&cur)[4], vec8 (&nxt)[4]) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's DMA and record loads of tile w
+    __syncthreads();                // every wavefront's DMA of tile w; tile w - 1 no longer read
+    const bool use = live(gi, qt);
+    if (w + 1 < nwork) {
+      issue_tile(gn, qn, (w + 1) & 1);
+      load_record(gn, qn, nxt);
+    }
+    if (use) {
+      const T* __restrict__ tQ = sQ[w & 1];
+      const T* __restrict__ tdO = sdO[w & 1];
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh) {
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+          const vec8 doa = ld_kmajor<T, false>(tdO, C::LDR, qh * 32 + mh * 16, 8, dt * 32, lane);
+          const vec8 qa = ld_kmajor<T, false>(tQ, C::LDR, qh * 32 + mh * 16, 8, dt * 32, lane);
+          dv[dt] = M::k16(doa, cur[mh], dv[dt]);
+          dk[dt] = M::k16(qa, cur[2 + mh], dk[dt]);
+        }
+      }
+    }
+    gi = gn;
+    qt = qn;
+    if (w + 1 < nwork) advance();
+  };
+  for (int w = 0; w < nwork; w += 2) {
+    step(w, ra, rb);
+    if (w + 1 < nwork) step(w + 1, rb, ra);
+  }
+
+  // The two query halves of a key group: wavefront (kg, 0) finishes dK, (kg, 1) dV.  Each
+  // hands the other its partial sum of the other output through LDS.
+  __syncthreads();  // every tile read (no DMA is in flight: the last step issued none)
+  float* give = reinterpret_cast<float*>(qh ? &sdO[0][0] : &sQ[0][0]) + kg * C::DT * 16 * 64;
+  const float* take = reinterpret_cast<const float*>(qh ? &sQ[0][0] : &sdO[0][0]) + kg * C::DT * 16 * 64;
+#pragma unroll
+  for (int i = 0; i < C::DT; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) give[(i * 16 + r) * 64 + lane] = qh ? dk[i][r] : dv[i][r];
+  __syncthreads();
+  const int key = kw0 + col;
+  if (key < Skv) {
+    using vec4 = typename VecOf<T, 4>::type;
+    T* __restrict__ out = static_cast<T*>(qh ? args.dv : args.dk) + kvoff + (size_t)key * D;
+    const float sc = qh ? 1.0f : args.sm_scale;
+#pragma unroll
+    for (int i = 0; i < C::DT; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4 v4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = g * 4 + e;
+          v4[e] = ((qh ? dv[i][r] : dk[i][r]) + take[(i * 16 + r) * 64 + lane]) * sc;
+        }
+        *reinterpret_cast<vec4*>(out + i * 32 + g * 8 + hh * 4) = __builtin_convertvector(v4, vec4);
+      }
+    }
+  }
+}
+
 }  // namespace
 
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream) {
+  // The score-store path (BwdArgs::scores set by the caller for the types and head dims
+  // that have it) replaces cb with the records and pass 2 with the store kernel.
+  constexpr bool kStore = sizeof(T) == 2 && (D == 64 || D == 128);
+  const bool store = kStore && a.scores != nullptr;
   if (stages & 1) {
     const int nQB = (a.Sq + kBM - 1) / kBM;
-    hipLaunchKernelGGL((coalibi_bwd_dq_kernel<T, D, CAUSAL>), dim3(nQB * a.B * a.Hq), dim3(256), 0, stream, a);
+    if (store) {
+      if constexpr (kStore)
+        hipLaunchKernelGGL((coalibi_bwd_dq_kernel<T, D, CAUSAL, true>), dim3(nQB * a.B * a.Hq), dim3(256), 0, stream,
+                           a);
+    } else {
+      hipLaunchKernelGGL((coalibi_bwd_dq_kernel<T, D, CAUSAL, false>), dim3(nQB * a.B * a.Hq), dim3(256), 0, stream,
+                         a);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
-    if constexpr (sizeof(T) == 2 && D >= 64) {  // the pair kernel splits D into 32-row halves
+    if (store) {
+      if constexpr (kStore) {
+        const int nKB = (a.Skv + kStoreBK - 1) / kStoreBK;
+        hipLaunchKernelGGL((coalibi_bwd_dkdv_store_kernel<T, D, CAUSAL>), dim3(nKB * a.B * a.Hkv), dim3(256), 0,
+                           stream, a);
+      }
+    } else if constexpr (sizeof(T) == 2 && D >= 64) {  // the pair kernel splits D into 32-row halves
       const int nKB = (a.Skv + kPairBK - 1) / kPairBK;
       hipLaunchKernelGGL((coalibi_bwd_dkdv_kernel<T, D, CAUSAL>), dim3(nKB * a.B * a.Hkv), dim3(64 * kPairWaves),
                          0, stream, a);

@@ -123,6 +123,17 @@ size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_k
   return round_up(rows * sizeof(float), 256) + zb_block_numel(batch, heads_q, seq_q, seq_kv) * sizeof(float);
 }
 
+size_t co_alibi_bwd_score_store_workspace_bytes(int dtype, int batch, int heads_q, int heads_kv, int seq_q,
+                                                int seq_kv, int head_dim, int causal) {
+  if (batch < 1 || heads_q < 1 || heads_kv < 1 || heads_q % heads_kv != 0 || seq_q < 1 || seq_kv < 1) return 0;
+  if ((dtype != CO_ALIBI_F16 && dtype != CO_ALIBI_BF16) || (head_dim != 64 && head_dim != 128)) return 0;
+  if (!coalibi::score_store_fits(heads_q, heads_kv, seq_q)) return 0;
+  const size_t rows = static_cast<size_t>(batch) * heads_q * seq_q;
+  return round_up(rows * sizeof(float), 256) + static_cast<size_t>(batch) * heads_q *
+                                                   coalibi::score_records_per_head(seq_q, seq_kv, causal != 0) *
+                                                   coalibi::kScoreRecordBytes;
+}
+
 size_t co_alibi_fwd_inference_workspace_bytes(int batch, int heads_q, int seq_kv) {
   if (batch < 1 || heads_q < 1 || seq_kv < 1) return 0;
   return round_up(static_cast<size_t>(batch) * heads_q * coalibi::zb_knorm_count(seq_kv) * sizeof(float), 256);
@@ -210,7 +221,7 @@ int co_alibi_fwd_inference(int dtype, const void* q, const void* k, const void* 
 
 namespace {
 
-// stages: 1 = pass 1 (dq, dsum, cb), 2 = pass 2 (dk, dv), 3 = both.
+// stages: 1 = pass 1 (dq, dsum, and cb or the score store), 2 = pass 2 (dk, dv), 3 = both.
 int bwd_impl(const char* fn, int stages, int dtype, const void* dout, const void* q, const void* k,
              const void* v, const void* o, const float* lse, const float* zb, const float* slopes, void* dq,
              void* dk, void* dv, void* workspace, size_t workspace_bytes, int batch, int heads_q,
@@ -225,8 +236,12 @@ int bwd_impl(const char* fn, int stages, int dtype, const void* dout, const void
     return rc;
   if ((stages & 1) && ((rc = check_ptr(fn, "o", o, 16)) || (rc = check_ptr(fn, "dq", dq, 16)))) return rc;
   if ((stages & 2) && ((rc = check_ptr(fn, "dk", dk, 16)) || (rc = check_ptr(fn, "dv", dv, 16)))) return rc;
+  // A workspace that holds the score store selects that path (where it exists).
+  const size_t need_store =
+      co_alibi_bwd_score_store_workspace_bytes(dtype, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal);
+  const bool store = need_store != 0 && workspace_bytes >= need_store;
   const size_t need = co_alibi_bwd_workspace_bytes(batch, heads_q, seq_q, seq_kv);
-  if (workspace_bytes < need)
+  if (!store && workspace_bytes < need)
     return fail(CO_ALIBI_EINVAL, std::string(fn) + ": workspace of " + std::to_string(workspace_bytes) +
                                      " bytes, need " + std::to_string(need));
   if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": sm_scale must be finite");
@@ -245,7 +260,13 @@ int bwd_impl(const char* fn, int stages, int dtype, const void* dout, const void
   a.dk = dk;
   a.dv = dv;
   a.dsum = static_cast<float*>(workspace);
-  a.cb = reinterpret_cast<float*>(static_cast<char*>(workspace) + round_up(rows * sizeof(float), 256));
+  char* const after_dsum = static_cast<char*>(workspace) + round_up(rows * sizeof(float), 256);
+  if (store) {  // the records follow dsum; no cb
+    a.scores = after_dsum;
+    a.score_head = coalibi::score_records_per_head(seq_q, seq_kv, causal != 0);
+  } else {
+    a.cb = reinterpret_cast<float*>(after_dsum);
+  }
   a.kstart = reinterpret_cast<const int*>(zb + zb_block_numel(batch, heads_q, seq_q, seq_kv));
   a.B = batch;
   a.Hq = heads_q;
@@ -490,6 +511,6 @@ int co_alibi_decode_noalloc(int dtype, const void* q, const void* k_cache, const
 
 const char* co_alibi_last_error(void) { return g_last_error.c_str(); }
 
-int co_alibi_abi_version(void) { return 3; }
+int co_alibi_abi_version(void) { return 4; }
 
 }  // extern "C"

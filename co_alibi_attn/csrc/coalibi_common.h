@@ -124,6 +124,26 @@ __device__ __forceinline__ V buffer_load_vec8(__amdgpu_buffer_rsrc_t r, int off)
 __device__ __forceinline__ void dma16_to_lds(__amdgpu_buffer_rsrc_t rsrc, void* lds, int voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
 }
+// The same DMA, issued by inline assembly so that the compiler does not track it.  The
+// compiled builtin counts as an LDS store the compiler cannot place, so it makes every later
+// LDS read of the wavefront wait for all DMA in flight, including DMA into another buffer;
+// with this form the caller orders the accesses itself: an explicit s_waitcnt vmcnt(0) and a
+// barrier before any wavefront reads what the DMA wrote, and a barrier after the last read
+// of a buffer before DMA into it is issued.  m0 holds the LDS base of the instruction.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_to_lds_untracked(__amdgpu_buffer_rsrc_t rsrc, void* lds, int voffset) {
+  const unsigned a = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(__attribute__((address_space(3))) void*)lds);
+  asm volatile(
+      "s_nop 4\n\t"
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(a), "v"(voffset), "s"(rsrc)
+      : "memory", "m0");
+}
+#pragma clang diagnostic pop
 // The same with the non-temporal cache policy (the "nt" bit, cache-policy value 2), for data
 // read exactly once: a stream of such loads sustains about 15 % more HBM bandwidth on
 // MI355X (6.9 against 6.0 TB/s in a read-only test of this access pattern).
@@ -276,6 +296,15 @@ struct DmaTile {
     for (int m = 0; m < SLOTS; ++m) {
       const int i = wave + NWAVES * m;
       if (i < NINSTR) dma16_to_lds(rsrc, lds + i * 64 * 16 / (int)sizeof(T), off[m]);
+    }
+  }
+  // The same through dma16_to_lds_untracked (its rules apply).
+  __device__ __forceinline__ void issue_untracked(const T* base, int row0, int nrows, T* lds, int wave) const {
+    const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(base + (size_t)row0 * D, min(max(nrows - row0, 0), ROWS) * D);
+#pragma unroll
+    for (int m = 0; m < SLOTS; ++m) {
+      const int i = wave + NWAVES * m;
+      if (i < NINSTR) dma16_to_lds_untracked(rsrc, lds + i * 64 * 16 / (int)sizeof(T), off[m]);
     }
   }
 };

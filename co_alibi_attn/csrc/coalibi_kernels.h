@@ -59,8 +59,35 @@ struct FwdArgs {
   float sc2;  // sm_scale * log2(e)
 };
 
+// Score store (16-bit types, D = 64 or 128): pass 1 writes the probabilities s and score
+// gradients dS of every tile it processes, and pass 2 reduces them into dK and dV instead of
+// recomputing them.  One record per (b*Hq + h, 32-key block jb, 32-row block qb) of a pair
+// that can be visible: 4096 bytes, the four 16 x 32 B operands of pass 2's products in MFMA
+// lane order -- s for rows 0-15, s for rows 16-31, dS for rows 0-15, dS for rows 16-31 of the
+// block; in each, lane l holds the 8 rows 8*(l/32) .. +7 of key l%32.  Records are key-block
+// major; causal: qb from jb to nQ32 - 1 (a row block below its key block holds no visible
+// pair), otherwise every qb.  Records of skipped tiles (tail skip) are never written or read.
+constexpr int kScoreRecordBytes = 4096;
+// Pass 2 keeps, per query head of a key head's group, one bit per 128-row block (rounded up to
+// 64 per head) of whether the forward processed its key block: at most this many 32-bit words.
+constexpr int kStoreProcessedWords = 512;
+inline bool score_store_fits(int Hq, int Hkv, int Sq) {
+  const int wph = (Sq + kSkipRows * 64 - 1) / (kSkipRows * 64) * 2;
+  return static_cast<long long>(Hq / Hkv) * wph <= kStoreProcessedWords;
+}
+__host__ __device__ inline size_t score_record(int jb, int qb, int nQ32, bool causal) {
+  if (!causal) return static_cast<size_t>(jb) * nQ32 + qb;
+  return static_cast<size_t>(jb) * nQ32 - static_cast<size_t>(jb) * (jb - 1) / 2 + (qb - jb);
+}
+inline size_t score_records_per_head(int Sq, int Skv, bool causal) {
+  const int nQ32 = (Sq + 31) / 32, nJB = (Skv + 31) / 32;
+  if (!causal) return static_cast<size_t>(nJB) * nQ32;
+  const int J = nJB < nQ32 ? nJB : nQ32;
+  return score_record(J, J, nQ32, true);  // records of the blocks before J
+}
+
 // Backward scratch: dsum (B*Hq, Sq) holds dO_i . O_i, cb (B*Hq, nZB, Sq)
-// holds sum over keys k < 32*J of dA_ik for every 32-key block J.
+// holds sum over keys k < 32*J of dA_ik for every 32-key block J (recompute path only).
 struct BwdArgs {
   const void* dout;
   const void* q;
@@ -76,6 +103,8 @@ struct BwdArgs {
   float* dsum;
   float* cb;
   const int* kstart;  // (B*Hq, nQB): keys left of kstart are skipped (see above)
+  void* scores;       // score store (above), or NULL: pass 2 recomputes s and dS from cb
+  size_t score_head;  // records per (b, h)
   int B, Hq, Hkv, Sq, Skv, nZB;
   float sc2;
   float sm_scale;
@@ -117,7 +146,7 @@ hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 template <typename T, int D>
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
 
-// stages: bit 0 = pass 1 (dq, dsum, cb), bit 1 = pass 2 (dk, dv; needs pass 1's dsum / cb).
+// stages: bit 0 = pass 1 (dq, dsum, and cb or the score store), bit 1 = pass 2 (dk, dv; needs pass 1's output).
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream);
 

@@ -11,6 +11,9 @@
 // allocates only through torch's caching allocator, so the operators can be captured in a HIP
 // graph.  co_alibi::fwd carries its backward as a C++ autograd kernel: dQ alone runs backward
 // pass 1 only (co_alibi::bwd_dq); any key / value gradient runs both passes (co_alibi::bwd).
+// co_alibi::bwd uses the score store (pass 1 keeps s and dS, pass 2 reduces them) where the
+// library has it and its workspace is at most CO_ALIBI_SCORE_STORE_LIMIT_MB megabytes (an
+// environment variable read once; 16384 by default, 0 turns the store off).
 // The shape functions for FakeTensor / meta tracing are registered from Python.
 #include <ATen/ATen.h>
 #include <ATen/core/dispatch/Dispatcher.h>
@@ -20,6 +23,7 @@
 #include <torch/library.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <tuple>
 
 #include "../../include/co_alibi.h"
@@ -102,6 +106,16 @@ std::tuple<Tensor, Tensor, Tensor> fwd_hip(const Tensor& q_in, const Tensor& k_i
 
 // --------------------------------------------------------------------------- backward
 
+// Largest workspace co_alibi::bwd takes for the score store.
+size_t score_store_limit() {
+  static const size_t limit = [] {
+    const char* e = std::getenv("CO_ALIBI_SCORE_STORE_LIMIT_MB");
+    const long long mb = e != nullptr && *e != '\0' ? std::atoll(e) : 16384;
+    return mb > 0 ? static_cast<size_t>(mb) << 20 : size_t{0};
+  }();
+  return limit;
+}
+
 // Shared set-up of both backward operators; stages 1 = pass 1 only (dq), 3 = both passes.
 std::tuple<Tensor, Tensor, Tensor> bwd_common(int stages, const Tensor& do_in, const Tensor& q_in, const Tensor& k_in,
                                               const Tensor& v_in, const Tensor& o_in, const Tensor& lse_in,
@@ -121,9 +135,14 @@ std::tuple<Tensor, Tensor, Tensor> bwd_common(int stages, const Tensor& do_in, c
   Tensor dq = at::empty_like(q);
   Tensor dk = stages & 2 ? at::empty_like(k) : Tensor();
   Tensor dv = stages & 2 ? at::empty_like(v) : Tensor();
-  const size_t ws_bytes = co_alibi_bwd_workspace_bytes(batch, heads_q, seq_q, seq_kv);
-  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
   const int code = dtype_code(q.scalar_type());
+  size_t ws_bytes = co_alibi_bwd_workspace_bytes(batch, heads_q, seq_q, seq_kv);
+  if (stages & 2) {
+    const size_t store_bytes =
+        co_alibi_bwd_score_store_workspace_bytes(code, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal ? 1 : 0);
+    if (store_bytes != 0 && store_bytes <= score_store_limit()) ws_bytes = store_bytes;
+  }
+  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
   const hipStream_t st = current_stream(q);
   if (stages & 2) {
     check(co_alibi_bwd(code, dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),

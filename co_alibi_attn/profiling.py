@@ -23,10 +23,12 @@ benchmark:
 Flop accounting.  The algorithmic work is the FlashAttention convention:
 forward 2 products (QK^T, PV) and backward 5 (S, dS, dV, dQ, dK), each
 2*B*Hq*D flops per (query, key) pair, halved for causal.  The forward kernel is
-charged its 2 products.  Backward pass 2 (dK, dV) is charged S, dS, dV and dK;
-pass 1 (dQ) is charged the dQ product only, and the S and dS products it
-recomputes are counted as issued, not charged, so the charged backward work is
-exactly 2.5x the forward's.
+charged its 2 products.  On the score-store path backward pass 1 issues S, dS
+and dQ and pass 2 (coalibi_bwd_dkdv_store_kernel) dV and dK: each is charged
+what it issues.  On the recompute path pass 2 (coalibi_bwd_dkdv_kernel) issues S,
+dS, dV and dK and is charged all four, and pass 1 is charged the dQ product only
+(its S and dS are counted as issued, not charged).  Either way the charged
+backward work is exactly 2.5x the forward's.
 """
 from __future__ import annotations
 
@@ -42,11 +44,12 @@ if __package__ in (None, ""):
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 
 CALIBRATION_BYTES = 1 << 30
-KERNELS = ("coalibi_fwd_kernel", "coalibi_bwd_dq_kernel", "coalibi_bwd_dkdv_kernel")
+KERNELS = ("coalibi_fwd_kernel", "coalibi_bwd_dq_kernel", "coalibi_bwd_dkdv_kernel")  # recompute path
+STORE_KERNELS = ("coalibi_fwd_kernel", "coalibi_bwd_dq_kernel", "coalibi_bwd_dkdv_store_kernel")
 DECODE_KERNELS = ("coalibi_decode_split_kernel", "coalibi_decode_merge_kernel")
 # co_alibi_fwd launches the key-norm kernel (max |k| per key chunk, for the tail skip) before
 # the forward kernel; per-launch timings of "coalibi_fwd_kernel" through the C ABI include it.
-NAMED_KERNELS = KERNELS + DECODE_KERNELS + ("coalibi_key_norm_kernel",)
+NAMED_KERNELS = KERNELS + STORE_KERNELS[2:] + DECODE_KERNELS + ("coalibi_key_norm_kernel",)
 # The two --pmc passes of the counter summary: at most 8 SQ and 2 GRBM counters each.
 COUNTER_PASSES = (
     ("SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU", "SQ_WAVES",
@@ -57,7 +60,18 @@ COUNTER_PASSES = (
 MI355X_CUS = 256   # 4 SIMDs each
 MI355X_XCDS = 8    # GRBM_GUI_ACTIVE is read once per XCD
 # (charged, issued) products per launch, in units of one GEMM of 2*B*Hq*D flops per visible pair.
-PRODUCTS = {"coalibi_fwd_kernel": (2, 2), "coalibi_bwd_dq_kernel": (1, 3), "coalibi_bwd_dkdv_kernel": (4, 4)}
+PRODUCTS = {
+    "recompute": {"coalibi_fwd_kernel": (2, 2), "coalibi_bwd_dq_kernel": (1, 3), "coalibi_bwd_dkdv_kernel": (4, 4)},
+    "store": {"coalibi_fwd_kernel": (2, 2), "coalibi_bwd_dq_kernel": (3, 3), "coalibi_bwd_dkdv_store_kernel": (2, 2)},
+}
+
+
+def score_store_limit() -> int:
+    """Largest backward workspace co_alibi::bwd takes for the score store, in bytes: the
+    CO_ALIBI_SCORE_STORE_LIMIT_MB environment variable (16384 by default, 0: never), as the
+    torch operator reads it."""
+    mb = int(os.environ.get("CO_ALIBI_SCORE_STORE_LIMIT_MB", "") or 16384)
+    return max(mb, 0) << 20
 
 
 def attention_flops(batch, heads_q, seq_q, seq_kv, head_dim, causal=True):
@@ -71,9 +85,10 @@ def attention_flops(batch, heads_q, seq_q, seq_kv, head_dim, causal=True):
 
 
 class KernelSet:
-    """Device buffers of one workload and a launcher per kernel, all through the C ABI on one stream."""
+    """Device buffers of one workload and a launcher per kernel, all through the C ABI on one stream.
+    ``path``: "store" or "recompute" backward; by default the one co_alibi::bwd takes."""
 
-    def __init__(self, w, device="cuda:0", seed: int = 0):
+    def __init__(self, w, device="cuda:0", seed: int = 0, path: str | None = None):
         import torch
 
         from co_alibi_attn import _native
@@ -89,11 +104,18 @@ class KernelSet:
         self.o = torch.empty_like(self.q)
         self.lse = torch.empty(B, Hq, S, device=dev, dtype=torch.float32)
         self.zb = torch.empty(lib.co_alibi_zb_numel(B, Hq, S, S), device=dev, dtype=torch.float32)
-        self.ws_bytes = lib.co_alibi_bwd_workspace_bytes(B, Hq, S, S)
+        code = _native.DTYPE_CODES[w.dtype]
+        store_bytes = lib.co_alibi_bwd_score_store_workspace_bytes(code, B, Hq, Hkv, S, S, D, int(w.causal))
+        if path is None:
+            path = "store" if 0 < store_bytes <= score_store_limit() else "recompute"
+        if path == "store" and store_bytes == 0:
+            raise ValueError(f"{w.name}: no score-store path for this dtype / head dim")
+        self.path = path
+        self.kernels = STORE_KERNELS if path == "store" else KERNELS
+        self.ws_bytes = store_bytes if path == "store" else lib.co_alibi_bwd_workspace_bytes(B, Hq, S, S)
         self.ws = torch.empty(self.ws_bytes, device=dev, dtype=torch.uint8)
         self.dq, self.dk, self.dv = (torch.empty_like(t) for t in (self.q, self.k, self.v))
         self.stream = torch.cuda.current_stream(dev)
-        code = _native.DTYPE_CODES[w.dtype]
         shape = (B, Hq, Hkv, S, S, D, int(w.causal), 1.0 / math.sqrt(D), self.stream.cuda_stream)
         p = lambda t: t.data_ptr()  # noqa: E731
 
@@ -118,19 +140,19 @@ class KernelSet:
             _native.check(lib.co_alibi_fwd_inference(code, p(self.q), p(self.k), p(self.v), p(self.lam), p(self.o),
                                                      p(self.ws_inf), self.ws_inf_bytes, *shape))
 
-        self.launch = dict(zip(KERNELS, (fwd, dq, dkdv)))
+        self.launch = dict(zip(self.kernels, (fwd, dq, dkdv)))
         self.launch["coalibi_fwd_kernel (inference)"] = fwd_inference
         self.gemm_flops = attention_flops(B, Hq, S, S, D, w.causal)[0] / 2.0  # one product
 
     def charged_flops(self, name: str) -> float:
-        return PRODUCTS[name][0] * self.gemm_flops
+        return PRODUCTS[self.path][name][0] * self.gemm_flops
 
     def issued_flops(self, name: str) -> float:
-        return PRODUCTS[name][1] * self.gemm_flops
+        return PRODUCTS[self.path][name][1] * self.gemm_flops
 
     def prime(self) -> None:
         """One launch of each kernel in pipeline order, so every input of every kernel is defined."""
-        for name in KERNELS:
+        for name in self.kernels:
             self.launch[name]()
 
     def time(self, name: str, reps: int) -> float:
@@ -256,7 +278,7 @@ def cmd_run(args) -> None:
     for _ in range(args.reps):
         ks.prime()
     torch.cuda.synchronize()
-    print(f"profiling run: {args.workload}, {args.reps} launches of each of {', '.join(KERNELS)}", flush=True)
+    print(f"profiling run: {args.workload}, {args.reps} launches of each of {', '.join(ks.kernels)}", flush=True)
 
 
 def _csv_rows(directory: str, suffix: str):

@@ -51,13 +51,25 @@ enum co_alibi_status {
  * sigmoid(sm_scale * q_i.k_j) over the visible keys j >= 32*J of row i; they take
  * the place of the reference's RowSigTotal (co_alibi_attn.py:37).  Then, per
  * 128-row block, the first key the forward processed (keys further left carry
- * softmax weights below 2^-64 of their row's total and are skipped by forward and
- * backward alike; zb is not written for them), and per 256-key chunk of each key
- * head, the largest |k|. */
+ * softmax weights below 2^-T of their row's total, T = 26 in fp16, 32 in bf16 and
+ * 64 in fp32, and are skipped by forward and backward alike; zb is not written for
+ * them), and per 256-key chunk of each key head, the largest |k|. */
 size_t co_alibi_zb_numel(int batch, int heads_q, int seq_q, int seq_kv);
 
 /* Bytes of device scratch co_alibi_bwd needs. */
 size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_kv);
+
+/* Bytes of device scratch that switch the backward to the score store: pass 1 keeps the
+ * probabilities and score gradients of every tile it processes, 4 KB per 32 x 32 block of
+ * pairs that can be visible (about 2 * Sq * Skv bytes per batch and query head when causal,
+ * twice that otherwise), and pass 2 reduces them into dk and dv instead of recomputing
+ * them.  0 when dtype / head_dim have no such path (fp16 and bf16 at head_dim 64 and 128
+ * have it) or when (heads_q / heads_kv) * ceil(seq_q / 8192) exceeds 256.  A workspace of at least this size selects the path; a smaller one (at least
+ * co_alibi_bwd_workspace_bytes) the recompute path.  co_alibi_bwd_dq and co_alibi_bwd_dkdv
+ * must then get the same workspace and size.  No counterpart in the reference, whose
+ * backward keeps per-query-block dK / dV partials instead (co_alibi_attn.py:83-133). */
+size_t co_alibi_bwd_score_store_workspace_bytes(int dtype, int batch, int heads_q, int heads_kv, int seq_q,
+                                                int seq_kv, int head_dim, int causal);
 
 /* Forward: writes o (B,Hq,Sq,D, dtype), lse (B,Hq,Sq, fp32 natural log-sum-exp
  * m_i + log(l_i), co_alibi_fwd_kernel.py:120) and zb.  The reference adds 1e-9
@@ -69,7 +81,7 @@ int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const f
                  int seq_kv, int head_dim, int causal, float sm_scale, void* stream);
 
 /* Forward for inference with the tail skip: o only (no lse or zb), skipping the keys
- * whose softmax weight is below 2^-64 of the row total as co_alibi_fwd does with its
+ * whose softmax weight is below 2^-T of the row total as co_alibi_fwd does with its
  * statistics (co_alibi_fwd with lse = zb = NULL computes every key).  workspace holds
  * co_alibi_fwd_inference_workspace_bytes(...) bytes (256-byte aligned): the largest |k|
  * per 256-key chunk of every key head.  No counterpart in the reference, whose forward
@@ -92,7 +104,7 @@ int co_alibi_bwd(int dtype, const void* dout, const void* q, const void* k, cons
 
 /* The two passes of co_alibi_bwd as separate calls, for callers that time or
  * schedule them apart.  co_alibi_bwd_dq writes dq and fills the workspace
- * (per-row dO.O and the per-32-key-block prefix of dA); co_alibi_bwd_dkdv
+ * (per-row dO.O and the per-32-key-block prefix of dA, or the score store); co_alibi_bwd_dkdv
  * then writes dk and dv from that workspace.  Issued in this order on one
  * stream they are exactly co_alibi_bwd.  The reference runs both in one
  * kernel (co_alibi_attn/co_alibi_bwd_kernel.py:17-146). */
@@ -153,7 +165,7 @@ int co_alibi_probe_mfma(void* ticks, void* sink, int blocks, int iters, void* st
 /* Message describing the last failed call on this thread ("" if none). */
 const char* co_alibi_last_error(void);
 
-/* ABI version of this header: 3 (co_alibi_fwd_inference; the zb buffer has kstart / knorm tails). */
+/* ABI version of this header: 4 (co_alibi_bwd_score_store_workspace_bytes). */
 int co_alibi_abi_version(void);
 
 #ifdef __cplusplus

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in co_alibi.h but not exported"
     assert sorted(_native.EXPORTS) == declared
-    assert lib.co_alibi_abi_version() == 3
+    assert lib.co_alibi_abi_version() == 4
 
 
 def test_sizes():
@@ -38,6 +38,30 @@ def test_sizes():
     rows = 4 * 16 * 4096
     assert lib.co_alibi_bwd_workspace_bytes(4, 16, 4096, 4096) == rows * 4 + 4 * 16 * 128 * 4096 * 4
     assert lib.co_alibi_bwd_workspace_bytes(1, 1, 3, 3) == 256 + 1 * 1 * 1 * 3 * 4
+
+
+def test_score_store_sizes():
+    """The score store: 4 KB per (32-key block, 32-row block) that can hold a visible pair,
+    after the per-row dO.O floats; only fp16 / bf16 at head dims 64 and 128 have it."""
+    lib = _native.lib()
+    f16, bf16, f32 = 1, 2, 0
+    rows = 4 * 16 * 4096
+    tri = 128 * 129 // 2  # causal: blocks (jb, qb) with qb >= jb of 128 x 128
+    assert lib.co_alibi_bwd_score_store_workspace_bytes(f16, 4, 16, 16, 4096, 4096, 128, 1) == rows * 4 + 64 * tri * 4096
+    assert lib.co_alibi_bwd_score_store_workspace_bytes(bf16, 4, 16, 4, 4096, 4096, 64, 0) == rows * 4 + 64 * 128 * 128 * 4096
+    # rectangular causal (top-left): Skv > Sq leaves key blocks past the last row block out
+    assert lib.co_alibi_bwd_score_store_workspace_bytes(f16, 1, 1, 1, 64, 1000, 64, 1) == 256 + 3 * 4096
+    # Sq > Skv: every key block, rows from its own block down
+    assert lib.co_alibi_bwd_score_store_workspace_bytes(f16, 1, 1, 1, 100, 40, 64, 1) == 512 + (4 + 3) * 4096
+    for dtype, d in ((f32, 128), (f16, 32), (f16, 256), (bf16, 16)):
+        assert lib.co_alibi_bwd_score_store_workspace_bytes(dtype, 1, 2, 2, 64, 64, d, 1) == 0
+    assert lib.co_alibi_bwd_score_store_workspace_bytes(f16, 0, 2, 2, 64, 64, 64, 1) == 0
+    # pass 2 keeps a processed bit per 128-row block of each grouped head: at most 256 heads
+    # per key head x 8192 rows (or fewer heads x more rows)
+    assert lib.co_alibi_bwd_score_store_workspace_bytes(f16, 1, 256, 1, 8192, 64, 64, 1) > 0
+    assert lib.co_alibi_bwd_score_store_workspace_bytes(f16, 1, 256, 1, 8193, 64, 64, 1) == 0
+    assert lib.co_alibi_bwd_score_store_workspace_bytes(f16, 1, 32, 1, 65536, 64, 64, 1) > 0
+    assert lib.co_alibi_bwd_score_store_workspace_bytes(f16, 1, 32, 1, 65537, 64, 64, 1) == 0
 
 
 def _fwd(lib, **over):

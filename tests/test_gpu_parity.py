@@ -103,6 +103,19 @@ def hip_fwd_raw(q, k, v, slopes, causal, sm_scale):
 
 # --------------------------------------------------------------------------- small shapes
 
+def bwd_workspace_bytes(lib, path, dtype, B, Hq, Hkv, Sq, Skv, D, causal):
+    """Workspace size that selects a backward path: "recompute" (pass 2 recomputes s and dS
+    from cb) or "store" (pass 1 keeps them in the score store)."""
+    if path == "recompute":
+        return lib.co_alibi_bwd_workspace_bytes(B, Hq, Sq, Skv)
+    n = lib.co_alibi_bwd_score_store_workspace_bytes(_native.DTYPE_CODES[dtype], B, Hq, Hkv, Sq, Skv, D, int(causal))
+    assert n > 0, "no score-store path for this dtype / head dim"
+    return n
+
+
+PATHS = ["recompute", "store"]
+
+
 def test_cpu_config_fp32_validation_mode():
     """BASELINE configs[0] in the fp32 validation mode: max-abs <= 1e-4."""
     w = WORKLOADS["cpu"]
@@ -167,8 +180,9 @@ def test_lse_and_penalty_statistics(dtype):
             assert err <= 1e-3 * max(1.0, S / 32), f"zb head {h} block {J}: {err}"
 
 
-def test_split_backward_equals_full():
-    """co_alibi_bwd_dq then co_alibi_bwd_dkdv == co_alibi_bwd, bit for bit."""
+@pytest.mark.parametrize("path", PATHS)
+def test_split_backward_equals_full(path):
+    """co_alibi_bwd_dq then co_alibi_bwd_dkdv == co_alibi_bwd, bit for bit, on either path."""
     lib = _native.lib()
     B, Hq, Hkv, S, D = 1, 4, 2, 190, 128
     dtype = torch.float16
@@ -176,7 +190,7 @@ def test_split_backward_equals_full():
     lam = ref.slopes(Hq, dtype=dtype).float().to(DEV)
     scale = 1.0 / math.sqrt(D)
     o, lse, zb = hip_fwd_raw(q, k, v, lam, True, scale)
-    ws_bytes = lib.co_alibi_bwd_workspace_bytes(B, Hq, S, S)
+    ws_bytes = bwd_workspace_bytes(lib, path, dtype, B, Hq, Hkv, S, S, D, True)
     st = torch.cuda.current_stream().cuda_stream
     outs = []
     for split in (False, True):
@@ -246,9 +260,10 @@ def test_inference_forward_equals_training_forward(dtype):
             assert (o_abi.float() - o_plain.float()).abs().max().item() <= 1e-6
 
 
+@pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["fp16", "bf16", "fp32"])
-def test_tail_skip(dtype, causal):
+def test_tail_skip(dtype, causal, path):
     """Slopes large enough that the forward stops early (keys whose weight is below 2^-26 (fp16),
     2^-32 (bf16) or 2^-64 (fp32) of their row's total are left out, and the backward passes
     leave out the same keys):
@@ -265,7 +280,9 @@ def test_tail_skip(dtype, causal):
     do = (do.float() * 0.5).to(dtype)
     lam = torch.tensor([4.0, 1.0, 0.25, 1e-3]).to(dtype).float()
     scale = 1.0 / math.sqrt(D)
-    print(f"tail skip {dtype} causal={causal}", flush=True)
+    if path == "store" and dtype == torch.float32:
+        pytest.skip("the score store is a 16-bit path")
+    print(f"tail skip {dtype} causal={causal} {path}", flush=True)
     qd, kd, vd, dod, lamd = (t.to(DEV) for t in (q, k, v, do, lam))
     o, lse, zb = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
     st = torch.cuda.current_stream().cuda_stream
@@ -273,7 +290,7 @@ def test_tail_skip(dtype, causal):
     _native.check(lib.co_alibi_fwd(_native.DTYPE_CODES[dtype], qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
                                    lamd.data_ptr(), o_plain.data_ptr(), 0, 0, B, Hq, Hkv, S, S, D, int(causal),
                                    scale, st))
-    ws_bytes = lib.co_alibi_bwd_workspace_bytes(B, Hq, S, S)
+    ws_bytes = bwd_workspace_bytes(lib, path, dtype, B, Hq, Hkv, S, S, D, causal)
     ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
     dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
     _native.check(lib.co_alibi_bwd(_native.DTYPE_CODES[dtype], dod.data_ptr(), qd.data_ptr(), kd.data_ptr(),
@@ -295,12 +312,13 @@ def test_tail_skip(dtype, causal):
     ro, _ = ref.forward(q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
     rdq, rdk, rdv = ref.backward(do.float(), q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
     assert_parity(tuple(t.float().cpu() for t in (o, dq, dk, dv)), (ro, rdq, rdk, rdv), TOL[dtype],
-                  f"tail skip causal={causal}", dtype)
+                  f"tail skip causal={causal} {path}", dtype)
 
 
+@pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
-def test_tail_skip_grouped_rectangular(dtype, causal):
+def test_tail_skip_grouped_rectangular(dtype, causal, path):
     """The tail skip with grouped query heads of mixed steepness (the key head's pass-2 work list
     mixes heads whose skipped ranges differ), Sq != Skv (top-left causal), two batches and
     D = 128: forward and backward against the oracle."""
@@ -310,11 +328,11 @@ def test_tail_skip_grouped_rectangular(dtype, causal):
     do = (do.float() * 0.5).to(dtype)
     lam = torch.tensor([3.0, 0.02, 1.0, 0.5, 0.002, 2.0]).to(dtype).float()
     scale = 1.0 / math.sqrt(D)
-    print(f"tail skip grouped {dtype} causal={causal}", flush=True)
+    print(f"tail skip grouped {dtype} causal={causal} {path}", flush=True)
     qd, kd, vd, dod, lamd = (t.to(DEV) for t in (q, k, v, do, lam))
     o, lse, zb = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
     st = torch.cuda.current_stream().cuda_stream
-    ws_bytes = lib.co_alibi_bwd_workspace_bytes(B, Hq, Sq, Skv)
+    ws_bytes = bwd_workspace_bytes(lib, path, dtype, B, Hq, Hkv, Sq, Skv, D, causal)
     ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
     dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
     _native.check(lib.co_alibi_bwd(_native.DTYPE_CODES[dtype], dod.data_ptr(), qd.data_ptr(), kd.data_ptr(),
@@ -328,7 +346,57 @@ def test_tail_skip_grouped_rectangular(dtype, causal):
     ro, _ = ref.forward(q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
     rdq, rdk, rdv = ref.backward(do.float(), q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
     assert_parity(tuple(t.float().cpu() for t in (o, dq, dk, dv)), (ro, rdq, rdk, rdv), TOL[dtype],
-                  f"tail skip grouped causal={causal}", dtype)
+                  f"tail skip grouped causal={causal} {path}", dtype)
+
+
+STORE_CASES = [  # B, Hq, Hkv, Sq, Skv, D, causal
+    (1, 2, 2, 64, 64, 64, True),
+    (2, 4, 2, 190, 190, 128, True),
+    (1, 4, 1, 150, 150, 64, False),
+    (1, 2, 2, 100, 300, 128, True),   # Skv > Sq: key blocks past the last row block have no records
+    (1, 2, 1, 300, 100, 64, True),    # Sq > Skv
+    (2, 2, 2, 33, 97, 128, False),
+    (1, 8, 2, 520, 520, 128, True),   # several work items per key block, group of 4
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("case", STORE_CASES, ids=lambda c: "B{}H{}/{}S{}x{}D{}{}".format(*c[:6], "c" if c[6] else "n"))
+def test_score_store_matches_recompute(case, dtype):
+    """The score-store backward against the recompute backward (same forward statistics) and
+    the oracle: dq is bit-identical (pass 1 computes it the same way on both paths), dk and dv
+    agree within the rounding of the recomputed scores, and both meet the bar."""
+    lib = _native.lib()
+    B, Hq, Hkv, Sq, Skv, D, causal = case
+    q, k, v, do = rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=31)
+    lam = ref.slopes(Hq, dtype=dtype).float()
+    scale = 1.0 / math.sqrt(D)
+    print(f"score store {case} {dtype}", flush=True)
+    qd, kd, vd, dod, lamd = (t.to(DEV) for t in (q, k, v, do, lam))
+    o, lse, zb = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
+    st = torch.cuda.current_stream().cuda_stream
+    outs = {}
+    for path in PATHS:
+        ws_bytes = bwd_workspace_bytes(lib, path, dtype, B, Hq, Hkv, Sq, Skv, D, causal)
+        ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+        dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+        _native.check(lib.co_alibi_bwd(_native.DTYPE_CODES[dtype], dod.data_ptr(), qd.data_ptr(), kd.data_ptr(),
+                                       vd.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), lamd.data_ptr(),
+                                       dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq,
+                                       Hkv, Sq, Skv, D, int(causal), scale, st))
+        torch.cuda.synchronize()
+        outs[path] = tuple(t.float().cpu() for t in (dq, dk, dv))
+    assert torch.equal(outs["store"][0], outs["recompute"][0])
+    for a, b, name in zip(outs["store"][1:], outs["recompute"][1:], ("dk", "dv")):
+        # the same bar as against the oracle: a flipped output rounding is one ulp of |b|
+        err = (a - b).abs().max().item()
+        bar = TOL[dtype] * max(1.0, b.abs().max().item() / REF_SCALE[dtype])
+        print(f"  store vs recompute {name}: {err:.3e} (bar {bar:.3g})", flush=True)
+        assert err <= bar, name
+    ro, _ = ref.forward(q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
+    rdq, rdk, rdv = ref.backward(do.float(), q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
+    for path in PATHS:
+        assert_parity((o.float().cpu(),) + outs[path], (ro, rdq, rdk, rdv), TOL[dtype], f"{path} {case}", dtype)
 
 
 def test_sm_scale_and_bias_max_arguments():
