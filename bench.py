@@ -11,7 +11,8 @@ Also measured in the same run:
     (forward, backward pass 1, backward pass 2); the longest one is reported
     in ``roofline`` against the dense fp16 MFMA peak, with the HBM traffic per
     launch that the rocprofv3 FETCH_SIZE/WRITE_SIZE passes recorded in
-    profiles/traffic_<workload>.md (null when that file is absent);
+    profiles/traffic_<workload>.md (null when that file is absent) and that traffic's
+    rate as a fraction of the 8 TB/s HBM peak (``hbm_frac``);
   * the box's sustained MFMA rate (``mfma_ceiling``): a probe kernel issuing only
     fp16 MFMAs on every CU for ~10 ms, its rate and clock (sustained MFMA-only load
     lowers the clock below the 2.4 GHz of the published peak).  It is context only:
@@ -374,7 +375,11 @@ def main():
         "coalibi_over_sdpa": None if sdpa_ms is None else round(ms_step / sdpa_ms, 3),
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),
-                     "traffic": None if traffic is None else round(traffic)},
+                     "traffic": None if traffic is None else round(traffic),
+                     # the same kernel's measured HBM rate (traffic over its median time) against
+                     # the 8 TB/s peak: the score-store path moves its records through HBM
+                     "hbm_frac": None if traffic is None else
+                     round(traffic / (per_kernel[dominant]["ms"] * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)},
     }
     if args.decode:
         out["decode"] = decode_bench(args)
