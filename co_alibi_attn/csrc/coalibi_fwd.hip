@@ -183,15 +183,23 @@ __global__ __launch_bounds__(256) void coalibi_key_norm_kernel(const T* __restri
     if (tid == 0) knorm[(size_t)bhk * nKC + c] = 0.f;
     return;
   }
-  const T* __restrict__ base = k + (size_t)bhk * Skv * D;
-  const int r1 = min((c + 1) * kNormKeys, Skv);
+  // Every load of the chunk goes out before any is used, through a buffer resource over the
+  // chunk's valid rows (rows past Skv read as zero, whose norm 0 leaves the maximum alone).
+  constexpr int NP = kNormKeys / RPP;  // passes over the chunk
+  const int r0 = c * kNormKeys;
+  const __amdgpu_buffer_rsrc_t rs = tile_rsrc(k + ((size_t)bhk * Skv + r0) * D, min(kNormKeys, Skv - r0) * D);
+  u32x4 x[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+    x[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((p * RPP + tid / CPR) * D + (tid % CPR) * CH) * (int)sizeof(T),
+                                                 0, 0);
   float best = 0.f;
-  for (int r = c * kNormKeys + tid / CPR; r < r1; r += RPP) {
-    const typename VecOf<T, CH>::type x =
-        __builtin_bit_cast(typename VecOf<T, CH>::type, ld16(base + (size_t)r * D + (tid % CPR) * CH));
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const typename VecOf<T, CH>::type xv = __builtin_bit_cast(typename VecOf<T, CH>::type, x[p]);
     float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < CH; ++e) ss = fmaf((float)x[e], (float)x[e], ss);
+    for (int e = 0; e < CH; ++e) ss = fmaf((float)xv[e], (float)xv[e], ss);
 #pragma unroll
     for (int off = CPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
     best = ss != ss ? ss : fmaxf(best, ss);

@@ -232,6 +232,9 @@ class FwdFunction : public torch::autograd::Function<FwdFunction> {
     ctx->saved_data["sm_scale"] = sm_scale;
     ctx->saved_data["with_stats"] = with_stats;
     ctx->mark_non_differentiable({lse, zb});
+    // lse and zb never get a gradient: without this the engine would fill zero tensors for them
+    // before every backward (zb is O(S^2 / 32) floats).
+    ctx->set_materialize_grads(false);
     return {o, lse, zb};
   }
 
