@@ -48,7 +48,7 @@ _SIGNATURES = {
     "co_alibi_bwd_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "co_alibi_bwd_score_store_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I, _I]),
     "co_alibi_fwd": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
-    "co_alibi_fwd_inference_workspace_bytes": (_Z, [_I, _I, _I]),
+    "co_alibi_fwd_inference_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "co_alibi_fwd_inference": (_I, [_I, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
     "co_alibi_bwd": (
         _I,
@@ -86,7 +86,7 @@ def lib() -> ctypes.CDLL:
         # The version first: a library of another ABI may lack some of the symbols below.
         handle.co_alibi_abi_version.restype = ctypes.c_int
         handle.co_alibi_abi_version.argtypes = []
-        if handle.co_alibi_abi_version() != 4:
+        if handle.co_alibi_abi_version() != 5:
             raise RuntimeError("co_alibi_attn: native library ABI version mismatch; "
                                "run `python -m co_alibi_attn._build`")
         for name, (res, args) in _SIGNATURES.items():

@@ -153,7 +153,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const int col = lane & 31, hh = lane >> 5;
   const int Sq = args.Sq, Skv = args.Skv;
   const int nQB = (Sq + kBM - 1) / kBM;
-  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hq, 1);
+  const WorkItem item = args.row_order ? table_item(args.row_order, blockIdx.x, args.B * args.Hq, gridDim.x)
+                                       : lpt_item(blockIdx.x, args.B * args.Hq, 1);
   const int bh = item.head;
   const int qb = nQB - 1 - item.rank;  // rank 0: the longest causal rows
   const int b = bh / args.Hq, hq = bh - b * args.Hq;
@@ -647,9 +648,11 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   const int kg = wave >> 1, qh = wave & 1;
   const int Sq = args.Sq, Skv = args.Skv;
   static_assert(sizeof(sSP) >= 2 * kMaxBalancedHeads * 4, "the head order is built in sSP");
-  const WorkItem item = balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
-                                      reinterpret_cast<float*>(&sSP[0][0][0]),
-                                      reinterpret_cast<int*>(&sSP[0][0][0]) + kMaxBalancedHeads, tid, 64 * kPairWaves);
+  const WorkItem item =
+      args.key_order ? table_item(args.key_order, blockIdx.x, args.B * args.Hkv, gridDim.x)
+                     : balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
+                                     reinterpret_cast<float*>(&sSP[0][0][0]),
+                                     reinterpret_cast<int*>(&sSP[0][0][0]) + kMaxBalancedHeads, tid, 64 * kPairWaves);
   const int bhk = item.head;               // b * Hkv + hkv
   const int kb = item.rank;                // rank 0: key block 0, seen by the most query rows
   const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;
@@ -888,9 +891,10 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
   const int kg = wave >> 1, qh = wave & 1;
   const int Sq = args.Sq, Skv = args.Skv;
   static_assert(sizeof(sQ[1]) >= 2 * kMaxBalancedHeads * 4, "the head order is built in sQ[1]");
-  const WorkItem item = balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
-                                      reinterpret_cast<float*>(sQ[1]),
-                                      reinterpret_cast<int*>(sQ[1]) + kMaxBalancedHeads, tid, 256);
+  const WorkItem item = args.key_order ? table_item(args.key_order, blockIdx.x, args.B * args.Hkv, gridDim.x)
+                                       : balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
+                                                       reinterpret_cast<float*>(sQ[1]),
+                                                       reinterpret_cast<int*>(sQ[1]) + kMaxBalancedHeads, tid, 256);
   const int bhk = item.head;  // b * Hkv + hkv
   const int kb = item.rank;   // rank 0: key block 0, seen by the most query rows
   const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;
@@ -1042,6 +1046,7 @@ hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream) {
   // that have it) replaces cb with the records and pass 2 with the store kernel.
   constexpr bool kStore = sizeof(T) == 2 && (D == 64 || D == 128);
   const bool store = kStore && a.scores != nullptr;
+  static_assert(kStoreBK == kOrderKeyBlock && kPairBK == kOrderKeyBlock, "key_order numbers 64-key blocks");
   if (stages & 1) {
     const int nQB = (a.Sq + kBM - 1) / kBM;
     if (store) {

@@ -114,7 +114,9 @@ extern "C" {
 size_t co_alibi_zb_numel(int batch, int heads_q, int seq_q, int seq_kv) {
   if (batch < 1 || heads_q < 1 || seq_q < 1 || seq_kv < 1) return 0;
   return zb_block_numel(batch, heads_q, seq_q, seq_kv) +
-         static_cast<size_t>(batch) * heads_q * (coalibi::zb_kstart_count(seq_q) + coalibi::zb_knorm_count(seq_kv));
+         static_cast<size_t>(batch) * heads_q *
+             (2 * coalibi::zb_kstart_count(seq_q) + coalibi::zb_knorm_count(seq_kv) +
+              coalibi::zb_key_block_count(seq_kv));
 }
 
 size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_kv) {
@@ -134,9 +136,11 @@ size_t co_alibi_bwd_score_store_workspace_bytes(int dtype, int batch, int heads_
                                                    coalibi::kScoreRecordBytes;
 }
 
-size_t co_alibi_fwd_inference_workspace_bytes(int batch, int heads_q, int seq_kv) {
-  if (batch < 1 || heads_q < 1 || seq_kv < 1) return 0;
-  return round_up(static_cast<size_t>(batch) * heads_q * coalibi::zb_knorm_count(seq_kv) * sizeof(float), 256);
+size_t co_alibi_fwd_inference_workspace_bytes(int batch, int heads_q, int seq_q, int seq_kv) {
+  if (batch < 1 || heads_q < 1 || seq_q < 1 || seq_kv < 1) return 0;
+  return round_up(static_cast<size_t>(batch) * heads_q *
+                      (coalibi::zb_knorm_count(seq_kv) + coalibi::zb_kstart_count(seq_q)) * sizeof(float),
+                  256);
 }
 
 }  // extern "C"
@@ -166,12 +170,18 @@ int fwd_impl(const char* fn, int dtype, const void* q, const void* k, const void
   a.o = o;
   a.lse = lse;
   a.zb = zb;
-  if (zb != nullptr) {  // kstart and knorm follow the zb blocks (coalibi_kernels.h)
+  const size_t bh = static_cast<size_t>(batch) * heads_q;
+  if (zb != nullptr) {  // kstart, knorm and the work orders follow the zb blocks (coalibi_kernels.h)
     float* tail = zb + zb_block_numel(batch, heads_q, seq_q, seq_kv);
     a.kstart = reinterpret_cast<int*>(tail);
-    a.knorm = tail + static_cast<size_t>(batch) * heads_q * coalibi::zb_kstart_count(seq_q);
-  } else {
+    a.knorm = tail + bh * coalibi::zb_kstart_count(seq_q);
+    int* orders = reinterpret_cast<int*>(
+        tail + bh * (coalibi::zb_kstart_count(seq_q) + coalibi::zb_knorm_count(seq_kv)));
+    a.row_order = orders;
+    a.key_order = orders + bh * coalibi::zb_kstart_count(seq_q);
+  } else if (knorm_ws != nullptr) {  // inference: the row order follows the norms
     a.knorm = knorm_ws;
+    a.row_order = reinterpret_cast<int*>(knorm_ws + bh * coalibi::zb_knorm_count(seq_kv));
   }
   a.B = batch;
   a.Hq = heads_q;
@@ -209,7 +219,7 @@ int co_alibi_fwd_inference(int dtype, const void* q, const void* k, const void* 
   const char* fn = "co_alibi_fwd_inference";
   int rc;
   if ((rc = check_ptr(fn, "workspace", workspace, 256))) return rc;
-  const size_t need = co_alibi_fwd_inference_workspace_bytes(batch, heads_q, seq_kv);
+  const size_t need = co_alibi_fwd_inference_workspace_bytes(batch, heads_q, seq_q, seq_kv);
   if (workspace_bytes < need)
     return fail(CO_ALIBI_EINVAL, std::string(fn) + ": workspace of " + std::to_string(workspace_bytes) +
                                      " bytes, need " + std::to_string(need));
@@ -267,7 +277,17 @@ int bwd_impl(const char* fn, int stages, int dtype, const void* dout, const void
   } else {
     a.cb = reinterpret_cast<float*>(after_dsum);
   }
-  a.kstart = reinterpret_cast<const int*>(zb + zb_block_numel(batch, heads_q, seq_q, seq_kv));
+  {  // the zb tail: kstart, knorm, then the work orders the forward wrote
+    const size_t bh = static_cast<size_t>(batch) * heads_q;
+    const float* tail = zb + zb_block_numel(batch, heads_q, seq_q, seq_kv);
+    a.kstart = reinterpret_cast<const int*>(tail);
+    const int* orders = reinterpret_cast<const int*>(tail + bh * (coalibi::zb_kstart_count(seq_q) +
+                                                                 coalibi::zb_knorm_count(seq_kv)));
+    a.row_order = coalibi::row_order_fits(batch, heads_q, seq_q) ? orders : nullptr;
+    a.key_order = coalibi::key_order_used(batch, heads_q, heads_kv, seq_kv)
+                      ? orders + bh * coalibi::zb_kstart_count(seq_q)
+                      : nullptr;
+  }
   a.B = batch;
   a.Hq = heads_q;
   a.Hkv = heads_kv;
@@ -511,6 +531,6 @@ int co_alibi_decode_noalloc(int dtype, const void* q, const void* k_cache, const
 
 const char* co_alibi_last_error(void) { return g_last_error.c_str(); }
 
-int co_alibi_abi_version(void) { return 4; }
+int co_alibi_abi_version(void) { return 5; }
 
 }  // extern "C"

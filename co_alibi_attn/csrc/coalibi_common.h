@@ -219,6 +219,14 @@ __device__ __forceinline__ WorkItem lpt_item(int id, int heads, int rotate) {
   const int rank = id / heads;
   return {(id - rank * heads + rank / rotate) % heads, rank};
 }
+// The item of work-group `id` from a work-order table (coalibi_kernels.h): entry id holds
+// rank * heads + head.  The entry is clamped into the grid's items, so a table that is not a
+// permutation cannot send a work-group out of bounds.
+__device__ __forceinline__ WorkItem table_item(const int* __restrict__ order, int id, int heads, int items) {
+  const int i = min(max(order[id], 0), items - 1);
+  const int rank = i / heads;
+  return {i - rank * heads, rank};
+}
 constexpr int kMaxBalancedHeads = 256;
 // `key` and `order` (kMaxBalancedHeads floats / ints of LDS scratch, free again on return)
 // hold the heads' slopes and rank order; every thread of the work-group calls this (three

@@ -164,21 +164,200 @@ __device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __re
   }
 }
 
+// ---------------------------------------------------------------------------
+// Work orders (coalibi_kernels.h), written by the first work-groups of the key-norm launch:
+// one sorts the forward's and pass 1's row blocks, one pass 2's key blocks, largest
+// predicted cost first.
+constexpr int kOrderBuckets = 256;  // cost classes: ceil(extent / 256) keys or rows each
+constexpr int kOrderLdsHeads = 1024;
+
+struct ScheduleArgs {
+  const float* slopes;
+  int* row_order;  // NULL: not written
+  int* key_order;  // NULL: not written
+  int B, Hq, Hkv, Sq, Skv;
+  int causal;
+  int rows_sorted, keys_sorted;  // 0: the table holds its index order (too large to sort, or unused)
+  float window;                  // order_window<T>()
+};
+
+// The lanes of the wavefront whose `b` equals this lane's (among the lanes with `ok`), matched
+// bit by bit with ballots.
+__device__ __forceinline__ unsigned long long same_bucket(int b, bool ok) {
+  unsigned long long peers = __ballot(ok);
+#pragma unroll
+  for (int bit = 0; (1 << bit) < kOrderBuckets; ++bit) {
+    const bool one = (b >> bit) & 1;
+    const unsigned long long m = __ballot(one);
+    peers &= one ? m : ~m;
+  }
+  return peers;
+}
+
+// Stable counting sort by one work-group of 256 threads: out[j] is the j-th of the n items in
+// decreasing bucket order, the items of one bucket in index order.  Wavefront w takes the w-th
+// quarter of the items; per wavefront, a chunk of 64 items is counted (and later placed) with
+// one LDS update per distinct bucket, by the lowest lane that holds it.  lds: 5 *
+// kOrderBuckets ints.
+template <typename F>
+__device__ void sort_items_desc(int n, const F& bucket, int* __restrict__ out, int* lds, int tid) {
+  constexpr int K = kOrderBuckets;
+  static_assert(K == 256, "one thread per bucket in the scan");
+  int* const cur = lds;          // [4][K]: per-wavefront counts, then per-wavefront cursors
+  int* const part = lds + 4 * K;  // [4]: per-wavefront scan totals
+  const int lane = tid & 63, wave = tid >> 6;
+  for (int j = tid; j < 4 * K; j += 256) cur[j] = 0;
+  __syncthreads();
+  const int per = (n + 3) / 4;
+  const int lo = min(wave * per, n), hi = min(lo + per, n);
+  int* const mine = cur + wave * K;
+  for (int base = lo; base < hi; base += 64) {
+    const int i = base + lane;
+    const bool ok = i < hi;
+    const int b = ok ? bucket(i) : 0;
+    const unsigned long long peers = same_bucket(b, ok);
+    if (ok && __popcll(peers & ((1ull << lane) - 1)) == 0) mine[b] += __popcll(peers);
+  }
+  __syncthreads();
+  // Thread t owns bucket K - 1 - t (descending): its total over the wavefronts, an exclusive
+  // scan over the threads, then each wavefront's cursor for the bucket.
+  const int bk = K - 1 - tid;
+  int c[4], tot = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) tot += (c[w] = cur[w * K + bk]);
+  int incl = tot;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) part[wave] = incl;
+  __syncthreads();
+  int start = incl - tot;
+  for (int w = 0; w < wave; ++w) start += part[w];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    cur[w * K + bk] = start;
+    start += c[w];
+  }
+  __syncthreads();
+  for (int base = lo; base < hi; base += 64) {
+    const int i = base + lane;
+    const bool ok = i < hi;
+    const int b = ok ? bucket(i) : 0;
+    const unsigned long long peers = same_bucket(b, ok);
+    if (ok) {
+      // LDS operations of the wavefront complete in program order: every lane reads the
+      // cursor before its lowest lane moves it.
+      const int before = __popcll(peers & ((1ull << lane) - 1));
+      const int at = mine[b];
+      out[at + before] = i;
+      if (before == 0) mine[b] = at + __popcll(peers);
+    }
+  }
+}
+
+// Per query head, the keys (or rows) a row block (or key block) keeps at most: window / slope,
+// or +inf for a slope that skips nothing (<= 0 or NaN).  Held in LDS for the first
+// kOrderLdsHeads heads; the others are computed where they are needed.
+struct HeadWindow {
+  const float* __restrict__ slopes;
+  const float* lds;
+  float window;
+  __device__ float operator()(int h) const {
+    if (h < kOrderLdsHeads) return lds[h];
+    const float lam = slopes[h];
+    return lam > 0.f ? window / lam : __builtin_inff();
+  }
+};
+
+// Cost class of a row block (item rank * heads + bh, rank 0 = the last row block): the keys
+// it processes, up to its diagonal (causal) and at most its head's window, in units of
+// ceil(Skv / kOrderBuckets) keys.
+struct RowCost {
+  HeadWindow win;
+  int heads, Hq, nQB, Skv, causal;
+  float unit;
+  __device__ int operator()(int i) const {
+    const int rank = i / heads, bh = i - rank * heads;
+    const int qb = nQB - 1 - rank;
+    const float keys = causal ? (float)min((qb + 1) * kSkipRows, Skv) : (float)Skv;
+    return min((int)(fminf(keys, win(bh % Hq)) / unit), kOrderBuckets - 1);
+  }
+};
+
+// Cost class of a 64-key block (item kb * heads + bh; one query head per key head): the query
+// rows that see it (causal: rows from its first key on), at most the head's window, in units
+// of ceil(Sq / kOrderBuckets) rows.
+struct KeyCost {
+  HeadWindow win;
+  int heads, H, Sq, causal;
+  float unit;
+  __device__ int operator()(int i) const {
+    const int kb = i / heads, bh = i - kb * heads;
+    const float rows = causal ? (float)max(Sq - kb * kOrderKeyBlock, 0) : (float)Sq;
+    return min((int)(fminf(rows, win(bh % H)) / unit), kOrderBuckets - 1);
+  }
+};
+
+// Work-group 0 writes the row order, work-group 1 the key order.  Every element of both tables
+// is written (the zb buffer is an output): a table that is not sorted holds its index order,
+// and the key table's room for B*Hq*nKB entries past its B*Hkv*nKB items holds zeros.
+__device__ void schedule_orders(const ScheduleArgs& s, int which, int tid) {
+  __shared__ int lds[5 * kOrderBuckets];
+  __shared__ float wlds[kOrderLdsHeads];
+  for (int h = tid; h < min(s.Hq, kOrderLdsHeads); h += 256) {
+    const float lam = s.slopes[h];
+    wlds[h] = lam > 0.f ? s.window / lam : __builtin_inff();
+  }
+  __syncthreads();
+  const HeadWindow win{s.slopes, wlds, s.window};
+  if (which == 0) {
+    const int nQB = (s.Sq + kSkipRows - 1) / kSkipRows;
+    const int n = nQB * s.B * s.Hq;
+    if (s.rows_sorted) {
+      const RowCost cost{win, s.B * s.Hq, s.Hq, nQB, s.Skv, s.causal,
+                         (float)((s.Skv + kOrderBuckets - 1) / kOrderBuckets)};
+      sort_items_desc(n, cost, s.row_order, lds, tid);
+    } else {
+      for (int i = tid; i < n; i += 256) s.row_order[i] = i;
+    }
+  } else {
+    const int nKB = zb_key_block_count(s.Skv);
+    const int n = nKB * s.B * s.Hkv;
+    if (s.keys_sorted) {
+      const KeyCost cost{win, s.B * s.Hkv, s.Hkv, s.Sq, s.causal,
+                         (float)((s.Sq + kOrderBuckets - 1) / kOrderBuckets)};
+      sort_items_desc(n, cost, s.key_order, lds, tid);
+    } else {
+      for (int i = tid; i < n; i += 256) s.key_order[i] = i;
+    }
+    for (int i = n + tid; i < nKB * s.B * s.Hq; i += 256) s.key_order[i] = 0;
+  }
+}
+
 // max over each chunk of kNormKeys keys of |k|_2, per key head: the key side of the tail
 // skip's bound.  One work-group per (head, chunk) over B*Hq heads: the buffer has room for
 // B*Hq rows, and rows past the B*Hkv key heads are written as zero, so every element of
 // the forward's statistics is written (deterministic outputs).  The D/CH lanes that hold one key row's 16-byte chunks
 // sum their squares with xor shuffles.  A NaN norm is kept (fmaxf would drop it), so a
 // non-finite key disables the skip for its head.
+// The first nSched work-groups of the launch write the work orders instead.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void coalibi_key_norm_kernel(const T* __restrict__ k, float* __restrict__ knorm,
-                                                               int Skv, int nKC, int nKeyHeads) {
+                                                               int Skv, int nKC, int nKeyHeads, int nSched,
+                                                               ScheduleArgs sched) {
   constexpr int CH = 16 / (int)sizeof(T);  // elements per 16-byte chunk
   constexpr int CPR = D / CH;              // chunks (lanes) per key row: 2 .. 32
   constexpr int RPP = 256 / CPR;           // key rows per pass of the work-group
   static_assert(CPR >= 2 && CPR <= 64 && (CPR & (CPR - 1)) == 0, "a key row spans a power-of-two lane group");
-  const int bhk = blockIdx.x / nKC, c = blockIdx.x - bhk * nKC;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if ((int)blockIdx.x < nSched) {
+    schedule_orders(sched, blockIdx.x, tid);
+    return;
+  }
+  const int id = blockIdx.x - nSched;
+  const int bhk = id / nKC, c = id - bhk * nKC;
   if (bhk >= nKeyHeads) {
     if (tid == 0) knorm[(size_t)bhk * nKC + c] = 0.f;
     return;
@@ -234,7 +413,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const int col = lane & 31, hh = lane >> 5;
   const int Sq = args.Sq, Skv = args.Skv;
   const int nQB = (Sq + kFwdBM - 1) / kFwdBM;
-  const WorkItem item = lpt_item(blockIdx.x, args.B * args.Hq, 1);
+  const WorkItem item = args.row_order ? table_item(args.row_order, blockIdx.x, args.B * args.Hq, gridDim.x)
+                                       : lpt_item(blockIdx.x, args.B * args.Hq, 1);
   const int bh = item.head;
   const int qb = nQB - 1 - item.rank;  // rank 0: the longest causal rows
   const int b = bh / args.Hq, hq = bh - b * args.Hq;
@@ -410,15 +590,24 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
   static_assert(kFwdBM == kSkipRows, "kstart entries are per forward row block");
+  FwdArgs f = a;
+  const bool rows_sorted = row_order_fits(a.B, a.Hq, a.Sq);
   if (a.knorm != nullptr) {
-    hipLaunchKernelGGL((coalibi_key_norm_kernel<T, D>), dim3(a.nKC * a.B * a.Hq), dim3(256), 0, stream,
-                       static_cast<const T*>(a.k), const_cast<float*>(a.knorm), a.Skv, a.nKC, a.B * a.Hkv);
+    const ScheduleArgs sched{a.slopes, a.row_order, a.key_order, a.B, a.Hq, a.Hkv, a.Sq, a.Skv, CAUSAL ? 1 : 0,
+                             rows_sorted ? 1 : 0, key_order_used(a.B, a.Hq, a.Hkv, a.Skv) ? 1 : 0,
+                             order_window<T>()};
+    // The key table needs the row table's work-group before it (work-group 1 writes it).
+    const int nSched = a.row_order == nullptr ? 0 : (a.key_order != nullptr ? 2 : 1);
+    hipLaunchKernelGGL((coalibi_key_norm_kernel<T, D>), dim3(nSched + a.nKC * a.B * a.Hq), dim3(256), 0, stream,
+                       static_cast<const T*>(a.k), const_cast<float*>(a.knorm), a.Skv, a.nKC, a.B * a.Hkv, nSched,
+                       sched);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
+  if (a.knorm == nullptr || !rows_sorted) f.row_order = nullptr;  // no sorted table: the fixed order
   const int nQB = (a.Sq + kFwdBM - 1) / kFwdBM;
   const int grid = nQB * a.B * a.Hq;
-  hipLaunchKernelGGL((coalibi_fwd_kernel<T, D, CAUSAL>), dim3(grid), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((coalibi_fwd_kernel<T, D, CAUSAL>), dim3(grid), dim3(256), 0, stream, f);
   return hipGetLastError();
 }
 

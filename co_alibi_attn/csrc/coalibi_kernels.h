@@ -18,7 +18,10 @@ constexpr float kLog2eHost = 1.4426950408889634f;
 //     2^-skip_log2 of its row's total in every row of the block (the tail skip below);
 //     the backward passes skip the same keys, and zb of those blocks is not written;
 //   knorm (B*Hq, nKC) fp32, nKC = ceil(Skv/kNormKeys): max_k |k|_2 over each chunk of
-//     kNormKeys keys of key head b*Hkv + h in its first B*Hkv rows, zero in the rest.
+//     kNormKeys keys of key head b*Hkv + h in its first B*Hkv rows, zero in the rest;
+//   row_order (B*Hq*nQB) int32: the work order of the forward and pass 1 (below);
+//   key_order (B*Hq*nKB) int32, nKB = ceil(Skv/64): the work order of pass 2 over its
+//     B*Hkv*nKB key blocks (written, and read, only when Hq == Hkv).
 //
 // Tail skip.  In the log2 domain a row's logit for key k is a_k = t_k - lam2 * z_k with
 // t_k = q.k * sm_scale * log2(e) and z_k = sum of sigmoids of the visible keys >= k.  The
@@ -45,6 +48,40 @@ constexpr float skip_log2() {
 constexpr int kSkipRows = 128;  // rows per kstart entry: the forward's and pass 1's row block
 inline int zb_kstart_count(int Sq) { return (Sq + kSkipRows - 1) / kSkipRows; }
 inline int zb_knorm_count(int Skv) { return (Skv + kNormKeys - 1) / kNormKeys; }
+constexpr int kOrderKeyBlock = 64;  // keys per pass-2 work-group (16-bit kernels)
+__host__ __device__ inline int zb_key_block_count(int Skv) { return (Skv + kOrderKeyBlock - 1) / kOrderKeyBlock; }
+
+// Work orders.  The tail skip makes a work-group's cost depend on its head's slope: a
+// 128-row block of a steep head processes a few key tiles, one of a flat head up to all of
+// them.  The hardware hands consecutive work-group ids to the 8 XCDs in turn and, within an
+// XCD, to its 4 shader engines in turn, and it dispatches in id order: when the engine
+// that the next id is bound for has no free slot, dispatch waits even if other engines are
+// idle.  Ids whose costs differ widely (the fixed orders of the kernels) therefore leave
+// engines idle; ids in decreasing order of cost keep every engine's queue alike.  The
+// key-norm launch writes such orders (coalibi_fwd.hip, schedule_rows / schedule_keys): entry
+// j of a table is the item the work-group with id j processes, item = rank * heads + head in
+// the fixed order's numbering, sorted by a cost predicted from the slope alone (the order is
+// not needed to be exact, only close): a row keeps about W = kOrderWindow / slope keys left
+// of its diagonal, where kOrderWindow = (T + 8) / (0.5 log2 e) for the threshold T of the
+// type (the sigmoid sum z grows by about 0.5 a key, and the skip fires once slope*z*log2 e
+// passes T plus the logit bound, a few units).
+// A table is sorted for at most this many items (the sort runs on one wavefront); larger
+// grids keep the fixed orders.
+constexpr long long kOrderMaxItems = 1 << 20;
+inline bool row_order_fits(int B, int Hq, int Sq) {
+  return static_cast<long long>(B) * Hq * zb_kstart_count(Sq) <= kOrderMaxItems;
+}
+inline bool key_order_fits(int B, int Hkv, int Skv) {
+  return static_cast<long long>(B) * Hkv * zb_key_block_count(Skv) <= kOrderMaxItems;
+}
+// Pass 2 follows key_order with one query head per key head only: with grouped heads the
+// sorted order measured slower than balanced_item (coalibi_common.h), which keeps runs of key
+// blocks of a head on one XCD.
+inline bool key_order_used(int B, int Hq, int Hkv, int Skv) { return Hq == Hkv && key_order_fits(B, Hkv, Skv); }
+template <typename T>
+constexpr float order_window() {
+  return (skip_log2<T>() + 8.0f) / (0.5f * kLog2eHost);
+}
 struct FwdArgs {
   const void* q;
   const void* k;
@@ -57,6 +94,10 @@ struct FwdArgs {
   const float* knorm;  // (B*Hq, nKC) chunk maxima of |k|, filled before the forward; NULL: no tail skip
   int B, Hq, Hkv, Sq, Skv, nZB, nKC;
   float sc2;  // sm_scale * log2(e)
+  // Work orders (above): written by the key-norm launch when not NULL (key_order only with
+  // row_order); the forward follows row_order when it is sorted (row_order_fits).
+  int* row_order;
+  int* key_order;
 };
 
 // Score store (16-bit types, D = 64 or 128): pass 1 writes the probabilities s and score
@@ -105,6 +146,8 @@ struct BwdArgs {
   const int* kstart;  // (B*Hq, nQB): keys left of kstart are skipped (see above)
   void* scores;       // score store (above), or NULL: pass 2 recomputes s and dS from cb
   size_t score_head;  // records per (b, h)
+  const int* row_order;  // pass 1's work order (above), or NULL: the fixed order
+  const int* key_order;  // pass 2's work order for 64-key work-groups, or NULL
   int B, Hq, Hkv, Sq, Skv, nZB;
   float sc2;
   float sm_scale;

@@ -94,8 +94,8 @@ std::tuple<Tensor, Tensor, Tensor> fwd_hip(const Tensor& q_in, const Tensor& k_i
     check(co_alibi_fwd(code, q.data_ptr(), k.data_ptr(), v.data_ptr(), sl.data_ptr<float>(), o.data_ptr(),
                        lse.data_ptr<float>(), zb.data_ptr<float>(), batch, heads_q, heads_kv, seq_q, seq_kv, head_dim,
                        causal ? 1 : 0, static_cast<float>(sm_scale), current_stream(q)));
-  } else {  // inference: the tail skip with only its key-norm scratch
-    const size_t ws_bytes = co_alibi_fwd_inference_workspace_bytes(batch, heads_q, seq_kv);
+  } else {  // inference: the tail skip with only its key-norm and work-order scratch
+    const size_t ws_bytes = co_alibi_fwd_inference_workspace_bytes(batch, heads_q, seq_q, seq_kv);
     Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
     check(co_alibi_fwd_inference(code, q.data_ptr(), k.data_ptr(), v.data_ptr(), sl.data_ptr<float>(), o.data_ptr(),
                                  ws.data_ptr(), ws_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim,

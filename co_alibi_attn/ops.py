@@ -76,8 +76,10 @@ else:
 def zb_numel(batch: int, heads_q: int, seq_q: int, seq_kv: int) -> int:
     """fp32 elements of the forward's penalty statistics (the value co_alibi_zb_numel of
     the C ABI returns): B*Hq * (ceil(Skv/32) * Sq  zb blocks, + ceil(Sq/128)  first
-    processed key per 128-row block, + ceil(Skv/256)  key-norm chunk maxima)."""
-    return batch * heads_q * (((seq_kv + 31) // 32) * seq_q + (seq_q + 127) // 128 + (seq_kv + 255) // 256)
+    processed key per 128-row block, + ceil(Skv/256)  key-norm chunk maxima, + ceil(Sq/128)
+    and ceil(Skv/64)  work orders of the row and key blocks)."""
+    return batch * heads_q * (((seq_kv + 31) // 32) * seq_q + 2 * ((seq_q + 127) // 128) + (seq_kv + 255) // 256
+                              + (seq_kv + 63) // 64)
 
 
 def _empty_stats(q: Tensor) -> Tensor:

@@ -133,7 +133,7 @@ class KernelSet:
                                                 p(self.zb), p(self.lam), p(self.dk), p(self.dv), p(self.ws),
                                                 self.ws_bytes, *shape))
 
-        self.ws_inf_bytes = lib.co_alibi_fwd_inference_workspace_bytes(B, Hq, S)
+        self.ws_inf_bytes = lib.co_alibi_fwd_inference_workspace_bytes(B, Hq, S, S)
         self.ws_inf = torch.empty(self.ws_inf_bytes, device=dev, dtype=torch.uint8)
 
         def fwd_inference():  # no LSE / zb: the forward of a caller that needs no backward (tail skip included)

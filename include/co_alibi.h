@@ -46,14 +46,15 @@ enum co_alibi_status {
 };
 
 /* Number of fp32 elements of the penalty statistics `zb` that co_alibi_fwd
- * writes and co_alibi_bwd reads: B*Hq * (ceil(Skv/32) * Sq + ceil(Sq/128) +
- * ceil(Skv/256)).  The first B*Hq*ceil(Skv/32)*Sq are zb[bh][J][i], the sum of
- * sigmoid(sm_scale * q_i.k_j) over the visible keys j >= 32*J of row i; they take
+ * writes and co_alibi_bwd reads: B*Hq * (ceil(Skv/32) * Sq + 2 * ceil(Sq/128) +
+ * ceil(Skv/256) + ceil(Skv/64)).  The first B*Hq*ceil(Skv/32)*Sq are zb[bh][J][i], the
+ * sum of sigmoid(sm_scale * q_i.k_j) over the visible keys j >= 32*J of row i; they take
  * the place of the reference's RowSigTotal (co_alibi_attn.py:37).  Then, per
  * 128-row block, the first key the forward processed (keys further left carry
  * softmax weights below 2^-T of their row's total, T = 26 in fp16, 32 in bf16 and
  * 64 in fp32, and are skipped by forward and backward alike; zb is not written for
- * them), and per 256-key chunk of each key head, the largest |k|. */
+ * them); per 256-key chunk of each key head, the largest |k|; and the order in which
+ * the kernels take their row and key blocks (int32), which the forward writes. */
 size_t co_alibi_zb_numel(int batch, int heads_q, int seq_q, int seq_kv);
 
 /* Bytes of device scratch co_alibi_bwd needs. */
@@ -84,9 +85,9 @@ int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const f
  * whose softmax weight is below 2^-T of the row total as co_alibi_fwd does with its
  * statistics (co_alibi_fwd with lse = zb = NULL computes every key).  workspace holds
  * co_alibi_fwd_inference_workspace_bytes(...) bytes (256-byte aligned): the largest |k|
- * per 256-key chunk of every key head.  No counterpart in the reference, whose forward
- * always saves its statistics (co_alibi_attn.py:35-57). */
-size_t co_alibi_fwd_inference_workspace_bytes(int batch, int heads_q, int seq_kv);
+ * per 256-key chunk of every key head and the order of the row blocks.  No counterpart in
+ * the reference, whose forward always saves its statistics (co_alibi_attn.py:35-57). */
+size_t co_alibi_fwd_inference_workspace_bytes(int batch, int heads_q, int seq_q, int seq_kv);
 int co_alibi_fwd_inference(int dtype, const void* q, const void* k, const void* v, const float* slopes,
                            void* o, void* workspace, size_t workspace_bytes, int batch, int heads_q,
                            int heads_kv, int seq_q, int seq_kv, int head_dim, int causal, float sm_scale,
@@ -165,7 +166,8 @@ int co_alibi_probe_mfma(void* ticks, void* sink, int blocks, int iters, void* st
 /* Message describing the last failed call on this thread ("" if none). */
 const char* co_alibi_last_error(void);
 
-/* ABI version of this header: 4 (co_alibi_bwd_score_store_workspace_bytes). */
+/* ABI version of this header: 5 (seq_q in co_alibi_fwd_inference_workspace_bytes; the
+ * work orders in zb). */
 int co_alibi_abi_version(void);
 
 #ifdef __cplusplus

@@ -227,7 +227,7 @@ void check_errors(hipStream_t stream) {
                                     (const float*)sl.p, o.p, o.p, o.p, ws.p, 0, 1, 2, 2, 8, 8, 64, 1, 0.125f, stream);
   expect("error: a workspace of 0 bytes is EINVAL", small_ws == CO_ALIBI_EINVAL &&
                                                         std::strstr(co_alibi_last_error(), "workspace") != nullptr);
-  expect("abi version 4", co_alibi_abi_version() == 4);
+  expect("abi version 5", co_alibi_abi_version() == 5);
 }
 
 }  // namespace

@@ -26,14 +26,15 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in co_alibi.h but not exported"
     assert sorted(_native.EXPORTS) == declared
-    assert lib.co_alibi_abi_version() == 4
+    assert lib.co_alibi_abi_version() == 5
 
 
 def test_sizes():
     lib = _native.lib()
     # zb: B*Hq * (ceil(Skv/32)*Sq blocks + ceil(Sq/128) kstart + ceil(Skv/256) key-norm chunks)
-    assert lib.co_alibi_zb_numel(4, 16, 4096, 4096) == 4 * 16 * (128 * 4096 + 32 + 16)
-    assert lib.co_alibi_zb_numel(1, 2, 5, 33) == 1 * 2 * (2 * 5 + 1 + 1)
+    # zb blocks, kstart, knorm, then the row and key work orders
+    assert lib.co_alibi_zb_numel(4, 16, 4096, 4096) == 4 * 16 * (128 * 4096 + 32 + 16 + 32 + 64)
+    assert lib.co_alibi_zb_numel(1, 2, 5, 33) == 1 * 2 * (2 * 5 + 1 + 1 + 1 + 1)
     assert lib.co_alibi_zb_numel(0, 2, 5, 33) == 0
     rows = 4 * 16 * 4096
     assert lib.co_alibi_bwd_workspace_bytes(4, 16, 4096, 4096) == rows * 4 + 4 * 16 * 128 * 4096 * 4
@@ -92,12 +93,15 @@ def test_fwd_argument_errors(over, code, msg):
 
 
 def test_fwd_inference_workspace():
-    """co_alibi_fwd_inference: its scratch is the key-norm chunk maxima (B*Hq*ceil(Skv/256) floats,
-    256-byte rounded), and a smaller or misaligned workspace is rejected before any launch."""
+    """co_alibi_fwd_inference: its scratch is the key-norm chunk maxima (B*Hq*ceil(Skv/256) floats)
+    and the row-block work order (B*Hq*ceil(Sq/128) ints), 256-byte rounded, and a smaller or
+    misaligned workspace is rejected before any launch."""
     lib = _native.lib()
-    assert lib.co_alibi_fwd_inference_workspace_bytes(4, 16, 4096) == 4 * 16 * 16 * 4
-    assert lib.co_alibi_fwd_inference_workspace_bytes(1, 3, 300) == 256
-    assert lib.co_alibi_fwd_inference_workspace_bytes(0, 3, 300) == 0
+    assert lib.co_alibi_fwd_inference_workspace_bytes(4, 16, 4096, 4096) == 4 * 16 * (16 + 32) * 4
+    assert lib.co_alibi_fwd_inference_workspace_bytes(1, 3, 300, 300) == 256
+    assert lib.co_alibi_fwd_inference_workspace_bytes(1, 3, 70000, 300) == 3 * (547 + 2) * 4 // 256 * 256 + 256
+    assert lib.co_alibi_fwd_inference_workspace_bytes(0, 3, 300, 300) == 0
+    assert lib.co_alibi_fwd_inference_workspace_bytes(1, 3, 0, 300) == 0
     P = 256
     rc = lib.co_alibi_fwd_inference(1, P, P, P, P, P, P, 0, 1, 2, 2, 8, 8, 64, 1, 0.125, None)
     assert rc == 1 and "workspace of 0 bytes, need 256" in lib.co_alibi_last_error().decode()

@@ -246,7 +246,7 @@ def test_inference_forward_equals_training_forward(dtype):
         _native.check(lib.co_alibi_fwd(_native.DTYPE_CODES[dtype], qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
                                        lam.data_ptr(), o_abi.data_ptr(), 0, 0, B, Hq, Hkv, Sq, Skv, D,
                                        int(causal), 1.0 / math.sqrt(D), st))
-        ws_bytes = lib.co_alibi_fwd_inference_workspace_bytes(B, Hq, Skv)
+        ws_bytes = lib.co_alibi_fwd_inference_workspace_bytes(B, Hq, Sq, Skv)
         ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
         _native.check(lib.co_alibi_fwd_inference(_native.DTYPE_CODES[dtype], qd.data_ptr(), kd.data_ptr(),
                                                  vd.data_ptr(), lam.data_ptr(), o_inf.data_ptr(), ws.data_ptr(),
