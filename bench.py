@@ -45,8 +45,11 @@ HBM_PEAK_GBS = 8000.0
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # The GPU's clock ramps up over the first ~20 steps of a fresh process (about 0.95 ms per
+    # step at first, 0.85 ms from the third 10-step round on, at the headline), so the default
+    # warm-up runs 50 untimed steps before the timed ones.
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="headline", choices=["headline", "gqa", "long", "cpu", "gpt"],
                     help="attention workload (BASELINE configs[0..3]) or the GPT training step (configs[4])")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
