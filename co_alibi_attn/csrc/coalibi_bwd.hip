@@ -30,6 +30,8 @@
 // Operands whose reduction runs over LDS rows (K^T in pass 1; Q^T, dO^T, s, dP
 // in pass 2) are read with ds_read_b64_tr_b16 from row-major tiles; the fp32
 // validation mode stores transposed copies instead.
+#include <type_traits>
+
 #include "coalibi_common.h"
 #include "coalibi_kernels.h"
 
@@ -236,19 +238,35 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   float* __restrict__ cb_row = STORE ? nullptr : args.cb + (size_t)bh * args.nZB * Sq + row;
   const int nQ32 = (Sq + 31) / 32;
 
-  for (int kt = kt0; kt < nkt; ++kt) {
-    __syncthreads();
+  // The memory counter completes in order and counts stores: a wait for a load also waits for
+  // every store issued before it, and where paths meet the compiler waits for the shortest
+  // count of any path.  So that the score-store records drain under the next tiles' work:
+  //  - each tile's zb is loaded during the tile before it, ahead of that tile's stores, into the
+  //    same register (a copy between registers would wait for the load);
+  //  - the K/V staging uses barriers that wait for LDS only (__syncthreads waits for the stores);
+  //  - the K/V and zb loads and the record stores are buffer operations issued on every path,
+  //    their ranges covering only what exists (the rest reads as zero or is dropped);
+  //  - the tiles that some wavefront skips (causal: the last ones) run in a loop of their own,
+  //    so the skip is not a path of the main loop.
+  auto load_zb = [&](int t) {  // this row's zb of tile t; zero past Sq and for t >= nkt
+    const int n = t < nkt ? max(min(Sq - wrow0, 32), 0) : 0;
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(args.zb + ((size_t)bh * args.nZB + t) * Sq + wrow0, n);
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, col * 4, 0, 0));
+  };
+  float zb = load_zb(kt0);
+  auto tile = [&](int kt, auto tail) __attribute__((always_inline)) {
+    lds_barrier();  // every wavefront's reads of the previous tile are done
     kregs.store_rows(sK, C::LDR, tid);
     vregs.store_rows(sV, C::LDR, tid);
     if constexpr (!C::kTr) kregs.store_cols(sKt, C::LDT1, tid);
-    __syncthreads();
-    if (kt + 1 < nkt) {
-      kregs.load(Kp, (kt + 1) * kBN, Skv, tid);
-      vregs.load(Vp, (kt + 1) * kBN, Skv, tid);
-    }
+    lds_barrier();  // the tile is in LDS
+    kregs.load(Kp, (kt + 1) * kBN, Skv, tid);  // past the last tile: zero rows, never used
+    vregs.load(Vp, (kt + 1) * kBN, Skv, tid);
     const int k0 = kt * kBN;
-    if (CAUSAL && k0 > wrow0 + 31) continue;  // every key of the tile is above this wavefront's rows
-    const float zb = row_ok ? zb_row[(size_t)kt * Sq] : 0.f;
+    if constexpr (decltype(tail)::value) {
+      // Every key of the tile is above this wavefront's rows, and so are the later tiles'.
+      if (CAUSAL && k0 > wrow0 + 31) return;
+    }
     const bool masked = (CAUSAL && k0 + kBN - 1 > wrow0) || (k0 + kBN > Skv) || (wrow0 + 32 > Sq);
 
     f32x16 sacc = f32x16{}, dacc;
@@ -272,6 +290,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     else
       dp_tile<T, false, CAUSAL>(sacc, dacc, zb, crun, lse2, k0 + hh * 16, row, hh, Skv, Sq, tile_sc2, lam, lam2,
                                 sb, pb, atot);
+    zb = load_zb(kt + 1);           // the next tile's (above)
+    asm volatile("" ::: "memory");  // issued here, before the tile's stores
     if constexpr (!STORE) {
       if (hh == 0 && row_ok) cb_row[(size_t)kt * Sq] = crun;
     }
@@ -293,31 +313,34 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     // Score store: after the dQ products, the tile's s and dS go through this wavefront's
     // LDS scratch ([row][key]) and back out in the operand order of pass 2, one 16-byte store
     // per lane and operand (a record is 4 KB written by one wavefront).  Rows past Sq have
-    // no record.
+    // no record: their stores fall outside an empty range.
     if constexpr (STORE) {
-      if (wrow0 < Sq) {
-        T* __restrict__ sc = sSc + wave * 2 * 32 * kScLD;
-        *reinterpret_cast<vec8*>(sc + col * kScLD + hh * 16) = sb[0];
-        *reinterpret_cast<vec8*>(sc + col * kScLD + hh * 16 + 8) = sb[1];
-        *reinterpret_cast<vec8*>(sc + (32 + col) * kScLD + hh * 16) = pb[0];
-        *reinterpret_cast<vec8*>(sc + (32 + col) * kScLD + hh * 16 + 8) = pb[1];
-        // The transpose reads take other lanes' values: keep the compiler from moving them
-        // above the writes (LDS operations of one wavefront execute in order).
-        asm volatile("" ::: "memory");
-        u32x4* rec = reinterpret_cast<u32x4*>(static_cast<char*>(args.scores) +
-                                              ((size_t)bh * args.score_head + score_record(kt, wrow0 / 32, nQ32, CAUSAL)) *
-                                                  kScoreRecordBytes) +
-                     lane;
-        // Non-temporal: each record is written once here and read once by pass 2 (about 8 %
-        // faster on both passes than write-back caching, measured).
+      T* __restrict__ sc = sSc + wave * 2 * 32 * kScLD;
+      *reinterpret_cast<vec8*>(sc + col * kScLD + hh * 16) = sb[0];
+      *reinterpret_cast<vec8*>(sc + col * kScLD + hh * 16 + 8) = sb[1];
+      *reinterpret_cast<vec8*>(sc + (32 + col) * kScLD + hh * 16) = pb[0];
+      *reinterpret_cast<vec8*>(sc + (32 + col) * kScLD + hh * 16 + 8) = pb[1];
+      // The transpose reads take other lanes' values: keep the compiler from moving them
+      // above the writes (LDS operations of one wavefront execute in order).
+      asm volatile("" ::: "memory");
+      const u32x4* rec = reinterpret_cast<const u32x4*>(
+          static_cast<const char*>(args.scores) +
+          ((size_t)bh * args.score_head + score_record(kt, wrow0 / 32, nQ32, CAUSAL)) * kScoreRecordBytes);
+      const __amdgpu_buffer_rsrc_t rs = tile_rsrc(rec, wrow0 < Sq ? kScoreRecordBytes / 16 : 0);
+      // Non-temporal: each record is written once here and read once by pass 2 (about 8 %
+      // faster on both passes than write-back caching, measured).
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          __builtin_nontemporal_store(
-              __builtin_bit_cast(u32x4, ld_kmajor<T, false>(sc + (m >> 1) * 32 * kScLD, kScLD, (m & 1) * 16, 8, 0, lane)),
-              &rec[m * 64]);
-      }
+      for (int m = 0; m < 4; ++m)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, ld_kmajor<T, false>(sc + (m >> 1) * 32 * kScLD, kScLD, (m & 1) * 16, 8, 0, lane)),
+            rs, (m * 64 + lane) * 16, 0, kCachePolicyNt);
     }
-  }
+  };
+  // Tiles that every wavefront of the block processes (causal: keys up to the block's first
+  // row), then the rest.
+  const int kt_main = CAUSAL ? max(kt0, min(nkt, q0 / kBN + 1)) : nkt;
+  for (int kt = kt0; kt < kt_main; ++kt) tile(kt, std::false_type{});
+  for (int kt = kt_main; kt < nkt; ++kt) tile(kt, std::true_type{});
 
   if (row_ok) {
     T* __restrict__ dQr = static_cast<T*>(args.dq) + qoff + (size_t)row * D;
