@@ -3,21 +3,27 @@
 A step is one forward + backward of ``co_alibi_attention`` over the headline
 workload (B=4, Hq=Hkv=16, S=4096, D=128, fp16,
 causal, q/k/v ~ 0.5 N(0,1), dO ~ N(0,1), seed 0), inputs resident in HBM.
-``value`` is algorithmic TFLOP/s of the step in the FlashAttention convention
-(fwd 4*B*H*S^2*D/2 for causal, bwd 2.5x fwd).  Prints one JSON line.
+``value`` is the step's effective TFLOP/s: algorithmic flops in the FlashAttention
+convention (fwd 4*B*H*S^2*D/2 for causal, bwd 2.5x fwd) over the step time, with the
+library's tail skip on (its default: keys whose softmax weight is provably negligible
+are left out).  Prints one JSON line.
 
 Also measured in the same run:
-  * each kernel alone through the C ABI with HIP events on the launch stream
-    (forward, backward pass 1, backward pass 2); the longest one is reported
-    in ``roofline`` against the dense fp16 MFMA peak, with the HBM traffic per
-    launch that the rocprofv3 FETCH_SIZE/WRITE_SIZE passes recorded in
-    profiles/traffic_<workload>.md (null when that file is absent) and that traffic's
-    rate as a fraction of the 8 TB/s HBM peak (``hbm_frac``);
+  * the full-work figures, with the tail skip off (every visible tile processed, as the
+    reference's kernels do): ``fwd_frac_peak`` and ``bwd_frac_peak`` are these, algorithmic
+    flops over kernel time against the dense fp16 MFMA peak -- the north star's fractions;
+  * each kernel alone through the C ABI with HIP events on the launch stream (forward,
+    backward pass 1, backward pass 2), skip on and off: its time, effective TFLOP/s, and
+    the flops its MFMA units actually issue, counted from the tiles the forward recorded as
+    processed (profiling.issued_k16); the longest skip-on kernel is reported in
+    ``roofline`` on issued flops, with the HBM traffic per launch that the rocprofv3
+    FETCH_SIZE/WRITE_SIZE passes recorded in profiles/traffic_<workload>.md (null when that
+    file is absent), that traffic's rate against the 8 TB/s HBM peak (``hbm_frac``), and
+    ``bound`` the resource with the larger fraction;
+  * the other BASELINE configs (``gqa``, ``long``: the same per-kernel figures; ``gpt``: the
+    GPT training step, tokens/s);
   * the box's sustained MFMA rate (``mfma_ceiling``): a probe kernel issuing only
-    fp16 MFMAs on every CU for ~10 ms, its rate and clock (sustained MFMA-only load
-    lowers the clock below the 2.4 GHz of the published peak).  It is context only:
-    the attention kernels mix VALU and MFMA work and run at a higher clock than the
-    probe, so every fraction in the line is against the published peak;
+    fp16 MFMAs on every CU for ~10 ms, its rate and clock (context only);
   * the CPU baseline: the repository's CPU restatement of model.py (oracle,
     fp32) on a time-bounded sample of the same workload;
   * decode steps (``co_alibi_decode``: one query per head against a key/value
@@ -60,6 +66,8 @@ def parse_args():
                     help="skip the torch SDPA (plain causal attention) comparison")
     ap.add_argument("--no-decode", dest="decode", action="store_false",
                     help="skip the decode-step measurement (co_alibi_decode over a key/value cache)")
+    ap.add_argument("--no-configs", dest="configs", action="store_false",
+                    help="skip the other BASELINE configs (gqa, long, gpt) in the attention run")
     return ap.parse_args()
 
 
@@ -138,8 +146,9 @@ def cpu_config_timing():
     return times[len(times) // 2] * 1e3
 
 
-def gpt_bench(args) -> None:
-    """one GPT training step (fwd + bwd + AdamW) per step, bf16 autocast."""
+def gpt_measure(steps: int, warmup: int) -> dict:
+    """the GPT training step (fwd + bwd + AdamW, bf16 autocast), timed over
+    ``steps`` steps after ``warmup``; also Co-ALiBi attention alone at the same shape."""
     import torch
 
     from co_alibi_attn.gpt import GPT, GPTConfig, make_optimizer, synthetic_batch, train_step
@@ -152,16 +161,16 @@ def gpt_bench(args) -> None:
     idx, tgt = synthetic_batch(cfg, batch, seq, seed=0, device=dev)
     print(f"[bench] GPT {cfg.n_layer}L d{cfg.d_model} H{cfg.n_head} vocab {cfg.vocab}: "
           f"{model.n_params() / 1e6:.1f}M params, B{batch} S{seq}", file=sys.stderr, flush=True)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         train_step(model, opt, idx, tgt)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         loss = train_step(model, opt, idx, tgt)
     end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms = start.elapsed_time(end) / steps
     # Attention alone at the same shape (fwd + bwd), to state its share of the step.
     from co_alibi_attn import co_alibi_attention
 
@@ -179,11 +188,11 @@ def gpt_bench(args) -> None:
     end.record()
     torch.cuda.synchronize()
     attn_ms = start.elapsed_time(end) / 10 * cfg.n_layer
+    print(f"[bench] GPT step {ms:.3f} ms, {batch * seq / (ms * 1e-3):.0f} tokens/s", file=sys.stderr, flush=True)
     out = {
         "metric": "GPT training step throughput (tokens/s), 12L d768 H12 Co-ALiBi, B8 S1024",
-        "value": round(batch * seq / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "value": round(batch * seq / (ms * 1e-3), 1), "unit": "tokens/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 3), "dtype": "bf16",
         "data": "synthetic (uniform-random token ids), random-init weights",
         "config": {"workload": "GPT training step (fwd+bwd+AdamW), BASELINE configs[4]", "layers": cfg.n_layer,
                    "d_model": cfg.d_model, "heads": cfg.n_head, "vocab": cfg.vocab, "global_batch": batch,
@@ -192,6 +201,15 @@ def gpt_bench(args) -> None:
         "attention_ms_per_step": round(attn_ms, 3),
         "attention_share": round(attn_ms / ms, 3),
     }
+    del model, opt
+    torch.cuda.empty_cache()
+    return out
+
+
+def gpt_bench(args) -> None:
+    """``--workload gpt``: the GPT training step as the line's metric."""
+    out = gpt_measure(args.steps, args.warmup)
+    out.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None})
     print(json.dumps(out), flush=True)
 
 
@@ -221,6 +239,121 @@ def decode_bench(args):
     return out
 
 
+def time_steps(step, steps: int, warmup: int) -> float:
+    """ms per step over ``steps`` calls of ``step`` after ``warmup`` untimed ones (HIP events)."""
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def kernel_figures(ks, args, peak: float) -> dict:
+    """Per-kernel medians of interleaved timing rounds (KernelSet ks, its skip setting), with
+    effective (algorithmic) and issued (from the recorded kstart) TFLOP/s."""
+    ks.prime()
+    import torch
+
+    torch.cuda.synchronize()
+    kstart = ks.kstart()
+    names = list(ks.kernels) + (["coalibi_fwd_kernel (inference)"] if ks.skip else [])
+    timed = {name: [] for name in names}
+    for _ in range(args.kernel_rounds):
+        for name in names:
+            timed[name].append(ks.time(name, args.kernel_reps))
+    out = {}
+    for name in names:
+        ms = sorted(timed[name])[len(timed[name]) // 2]
+        charged = ks.charged_flops("coalibi_fwd_kernel" if name.endswith("(inference)") else name)
+        issued = ks.issued_flops(name, kstart)
+        out[name] = {"ms": round(ms, 4),
+                     "effective_tflops": round(charged / (ms * 1e-3) / 1e12, 2),
+                     "charged_gflop": round(charged / 1e9, 2),
+                     "issued_gflop": None if issued is None else round(issued / 1e9, 2),
+                     "issued_tflops": None if issued is None else round(issued / (ms * 1e-3) / 1e12, 2),
+                     "mfma_frac": None if issued is None else round(issued / (ms * 1e-3) / 1e12 / peak, 4)}
+    return out
+
+
+def attention_measure(w, args, dev, detail: bool) -> dict:
+    """One attention workload: the drop-in step (skip on and off) and the three kernels through the
+    C ABI (skip on and off).  ``detail`` adds the inference forward and the processed share."""
+    import torch
+
+    from co_alibi_attn import _native, co_alibi_attention
+    from co_alibi_attn.profiling import KernelSet, attention_flops
+
+    dtype_name = {torch.float16: "fp16", torch.bfloat16: "bf16", torch.float32: "fp32"}[w.dtype]
+    peak = MFMA_PEAK_TFLOPS[dtype_name]
+    fwd_flops, bwd_flops = attention_flops(w.batch, w.heads_q, w.seq, w.seq, w.head_dim, w.causal)
+    from co_alibi_attn.workloads import make_inputs
+
+    q, k, v, do = make_inputs(w, seed=0, device=dev)
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+    print(f"[bench] workload {w.name}: B{w.batch} Hq{w.heads_q} Hkv{w.heads_kv} S{w.seq} D{w.head_dim} "
+          f"{dtype_name} causal={w.causal}", file=sys.stderr, flush=True)
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        o = co_alibi_attention(q, k, v, causal=w.causal, bias_max=w.bias_max)
+        o.backward(do)
+
+    res = {"config": {"batch": w.batch, "heads_q": w.heads_q, "heads_kv": w.heads_kv, "seq_len": w.seq,
+                      "head_dim": w.head_dim, "dtype": dtype_name, "causal": w.causal, "bias_max": w.bias_max}}
+    steps, warmup = (args.steps, args.warmup) if detail else (max(args.steps // 4, 10), max(args.warmup // 5, 5))
+    res["ms_per_step"] = round(time_steps(step, steps, warmup), 4)
+    with _native.tail_skip(False):
+        res["ms_per_step_full_work"] = round(time_steps(step, steps, warmup), 4)
+    print(f"[bench] {w.name} step {res['ms_per_step']:.3f} ms (tail skip), {res['ms_per_step_full_work']:.3f} ms "
+          f"(full work)", file=sys.stderr, flush=True)
+    res["effective_tflops"] = round((fwd_flops + bwd_flops) / (res["ms_per_step"] * 1e-3) / 1e12, 2)
+    del q, k, v, do
+
+    ks = KernelSet(w, dev)
+    ks.skip = True
+    on = kernel_figures(ks, args, peak)
+    kstart = ks.kstart()
+    ks.skip = False
+    off = kernel_figures(ks, args, peak)
+    fwd_name, p1, p2 = ks.kernels
+    res["backward_path"] = ks.path
+    res["kernels"] = on
+    res["kernels_full_work"] = off
+
+    def fracs(kern):
+        fwd_ms = kern[fwd_name]["ms"]
+        bwd_ms = kern[p1]["ms"] + kern[p2]["ms"]
+        return {"fwd_ms": fwd_ms, "bwd_ms": round(bwd_ms, 4),
+                "fwd_tflops": round(fwd_flops / (fwd_ms * 1e-3) / 1e12, 2),
+                "bwd_tflops": round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 2),
+                "fwd_frac_peak": round(fwd_flops / (fwd_ms * 1e-3) / 1e12 / peak, 4),
+                "bwd_frac_peak": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / peak, 4)}
+
+    res["full_work"] = fracs(off)
+    res["tail_skip"] = fracs(on)
+    import numpy as np
+
+    from co_alibi_attn.profiling import issued_k16
+
+    full = issued_k16(fwd_name, np.zeros_like(kstart), w.batch, w.heads_q, w.heads_kv, w.seq, w.seq, w.head_dim,
+                      w.causal)
+    res["tail_skip"]["forward_tiles_processed"] = round(
+        issued_k16(fwd_name, kstart, w.batch, w.heads_q, w.heads_kv, w.seq, w.seq, w.head_dim, w.causal) / full, 4)
+    print(f"[bench] {w.name} full work: {json.dumps(res['full_work'])}", file=sys.stderr, flush=True)
+    print(f"[bench] {w.name} tail skip: {json.dumps(res['tail_skip'])}", file=sys.stderr, flush=True)
+    res["_ks"] = ks
+    return res
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -234,119 +367,51 @@ def main():
 
     import torch
 
-    from co_alibi_attn import co_alibi_attention
-    from co_alibi_attn.profiling import attention_flops
-    from co_alibi_attn.workloads import WORKLOADS, make_inputs
+    from co_alibi_attn.profiling import attention_flops, read_traffic
+    from co_alibi_attn.workloads import WORKLOADS
 
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
-    dtype_name = {torch.float16: "fp16", torch.bfloat16: "bf16", torch.float32: "fp32"}[w.dtype]
-    q, k, v, do = make_inputs(w, seed=0, device=dev)
-    q.requires_grad_(True)
-    k.requires_grad_(True)
-    v.requires_grad_(True)
-    fwd_flops, bwd_flops = attention_flops(w.batch, w.heads_q, w.seq, w.seq, w.head_dim, w.causal)
-    print(f"[bench] workload {w.name}: B{w.batch} Hq{w.heads_q} Hkv{w.heads_kv} S{w.seq} D{w.head_dim} "
-          f"{dtype_name} causal={w.causal}", file=sys.stderr, flush=True)
-
-    def step():
-        q.grad = k.grad = v.grad = None
-        o = co_alibi_attention(q, k, v, causal=w.causal, bias_max=w.bias_max)
-        o.backward(do)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = start.elapsed_time(end) / args.steps
-    value = (fwd_flops + bwd_flops) / (ms_step * 1e-3) / 1e12
-    print(f"[bench] {args.steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f} s)", file=sys.stderr, flush=True)
-
-    # Per-kernel timing through the C ABI, HIP events on the launch stream.
-    from co_alibi_attn.profiling import KernelSet, read_traffic
-
-    B, Hq, Hkv, S, D = w.batch, w.heads_q, w.heads_kv, w.seq, w.head_dim
-    ks = KernelSet(w, dev)
-    ks.prime()
-    torch.cuda.synchronize()
-    # Rounds of every kernel in turn, median per kernel: the first launches after the step loop
-    # run slower (clock and cache state), and interleaving keeps the kernels comparable.
-    timed = {name: [] for name in (*ks.kernels, "coalibi_fwd_kernel (inference)")}
-    for _ in range(args.kernel_rounds):
-        for name in timed:
-            timed[name].append(ks.time(name, args.kernel_reps))
-    med = {name: sorted(v)[len(v) // 2] for name, v in timed.items()}
-    per_kernel = {}
-    for name in ks.kernels:
-        ms = med[name]
-        per_kernel[name] = {"ms": round(ms, 4),
-                            "tflops": round(ks.charged_flops(name) / (ms * 1e-3) / 1e12, 2),
-                            "charged_gflop": round(ks.charged_flops(name) / 1e9, 2),
-                            "issued_gflop": round(ks.issued_flops(name) / 1e9, 2)}
-    fwd_inference_ms = med["coalibi_fwd_kernel (inference)"]
-    fwd_ms = per_kernel["coalibi_fwd_kernel"]["ms"]
-    bwd_ms = per_kernel[ks.kernels[1]]["ms"] + per_kernel[ks.kernels[2]]["ms"]
-    dominant = max(per_kernel, key=lambda n: per_kernel[n]["ms"])
+    head = attention_measure(w, args, dev, detail=True)
+    ks = head.pop("_ks")
+    dtype_name = head["config"]["dtype"]
     peak = MFMA_PEAK_TFLOPS[dtype_name]
-    achieved = per_kernel[dominant]["tflops"]
-    traffic = read_traffic(os.path.join(ROOT, "profiles", f"traffic_{w.name}.md")).get(dominant)
-    print(f"[bench] per-kernel: {json.dumps(per_kernel)}", file=sys.stderr, flush=True)
+    fwd_flops, bwd_flops = attention_flops(w.batch, w.heads_q, w.seq, w.seq, w.head_dim, w.causal)
+    on, full, skip = head["kernels"], head["full_work"], head["tail_skip"]
 
-    # The published peak assumes 2.4 GHz.  The box's own MFMA ceiling: a probe kernel that
-    # issues only fp16 MFMAs on every CU for ~10 ms (its clock is the shader-clock /
-    # real-time counter ratio; sustained MFMA load lowers the clock).
+    # The roofline of the step's dominant kernel (skip on, as `value` is measured): its issued
+    # MFMA work and its HBM traffic, each against its peak; `bound` is the larger fraction.
+    names = [n for n in ks.kernels]
+    dominant = max(names, key=lambda n: on[n]["ms"])
+    traffic = read_traffic(os.path.join(ROOT, "profiles", f"traffic_{w.name}.md")).get(dominant)
+    mfma_frac = on[dominant]["mfma_frac"]
+    hbm_frac = None if traffic is None else traffic / (on[dominant]["ms"] * 1e-3) / (HBM_PEAK_GBS * 1e9)
+    bound = "hbm" if hbm_frac is not None and hbm_frac > mfma_frac else "mfma"
+    if bound == "mfma":
+        roof = {"bound": "mfma", "achieved": on[dominant]["issued_tflops"], "peak": peak, "unit": "TFLOP/s",
+                "frac": mfma_frac}
+    else:
+        gbs = traffic / (on[dominant]["ms"] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(hbm_frac, 4)}
+    roof.update({"kernel": dominant, "traffic": None if traffic is None else round(traffic),
+                 "mfma_frac_issued": mfma_frac,
+                 "hbm_frac": None if hbm_frac is None else round(hbm_frac, 4),
+                 "effective_tflops": on[dominant]["effective_tflops"]})
+
     from co_alibi_attn.profiling import mfma_probe
 
     probe_tflops, clock_ghz = mfma_probe(dev)
     print(f"[bench] MFMA probe: {probe_tflops:.0f} TFLOP/s, clock {clock_ghz:.3f} GHz", file=sys.stderr, flush=True)
+    del ks
+    torch.cuda.empty_cache()
 
     sdpa_ms, sdpa_mode = None, None
     if args.sdpa:
-        # Plain causal attention at the same shape and dtype (torch SDPA on ROCm), fwd + bwd:
-        # the cost of Co-ALiBi relative to ordinary attention.  Grouped heads go in with
-        # enable_gqa; where that path is unavailable, K and V are expanded to the query heads
-        # outside the timed region (the gradients then stay per query head).
-        import torch.nn.functional as F
+        sdpa_ms, sdpa_mode = sdpa_measure(w, args, dev)
 
-        qs, ks_, vs = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
-        gqa = w.heads_q != w.heads_kv
-
-        def sdpa_step(kk, vv, **kw):
-            qs.grad = ks_.grad = vs.grad = None
-            F.scaled_dot_product_attention(qs, kk, vv, is_causal=w.causal, **kw).backward(do)
-
-        run = lambda: sdpa_step(ks_, vs)  # noqa: E731
-        sdpa_mode = "mha"
-        if gqa:
-            try:
-                sdpa_step(ks_, vs, enable_gqa=True)
-                run = lambda: sdpa_step(ks_, vs, enable_gqa=True)  # noqa: E731
-                sdpa_mode = "enable_gqa"
-            except RuntimeError:
-                g = w.heads_q // w.heads_kv
-                kx = ks_.detach().repeat_interleave(g, dim=1).requires_grad_(True)
-                vx = vs.detach().repeat_interleave(g, dim=1).requires_grad_(True)
-                run = lambda: sdpa_step(kx, vx)  # noqa: E731
-                sdpa_mode = "expanded kv"
-        for _ in range(3):
-            run()
-        torch.cuda.synchronize()
-        start.record()
-        for _ in range(args.steps):
-            run()
-        end.record()
-        torch.cuda.synchronize()
-        sdpa_ms = start.elapsed_time(end) / args.steps
-        del qs, ks_, vs
-        print(f"[bench] torch SDPA causal fwd+bwd ({sdpa_mode}): {sdpa_ms:.3f} ms/step", file=sys.stderr, flush=True)
-
+    ms_step = head["ms_per_step"]
+    value = (fwd_flops + bwd_flops) / (ms_step * 1e-3) / 1e12
     out = {
         "metric": "fwd and bwd TFLOPS (and % of MFMA peak) at B4 H16 S4096 D128 fp16 causal",
         "value": round(value, 2),
@@ -354,36 +419,45 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
+        "ms_per_step": ms_step,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": dtype_name,
         "data": "synthetic (seeded N(0,1) inputs of the BASELINE shape)",
-        "config": {"workload": f"co_alibi_attention fwd+bwd, {w.name}", "batch": B, "heads_q": Hq,
-                   "heads_kv": Hkv, "seq_len": S, "head_dim": D, "causal": w.causal, "bias_max": w.bias_max},
-        "fwd_ms": fwd_ms,
-        "bwd_ms": round(bwd_ms, 4),
-        "fwd_tflops": round(fwd_flops / (fwd_ms * 1e-3) / 1e12, 2),
-        "bwd_tflops": round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 2),
-        "fwd_frac_peak": round(fwd_flops / (fwd_ms * 1e-3) / 1e12 / peak, 4),
-        "fwd_inference_ms": round(fwd_inference_ms, 4),
-        "bwd_frac_peak": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / peak, 4),
-        "ref_convention_tflops": {"fwd": round(2 * fwd_flops / (fwd_ms * 1e-3) / 1e12, 2),
-                                  "bwd": round(4 * fwd_flops / (bwd_ms * 1e-3) / 1e12, 2)},
-        "kernels": per_kernel,
+        "config": {"workload": f"co_alibi_attention fwd+bwd, {w.name}", "batch": w.batch, "heads_q": w.heads_q,
+                   "heads_kv": w.heads_kv, "seq_len": w.seq, "head_dim": w.head_dim, "causal": w.causal,
+                   "bias_max": w.bias_max},
+        "value_note": "effective TFLOP/s (algorithmic flops over the step time) with the tail skip on; "
+                      "fwd_frac_peak / bwd_frac_peak are with the tail skip off (full work)",
+        "ms_per_step_full_work": head["ms_per_step_full_work"],
+        # the north star's fractions: full work (every visible tile), algorithmic flops / kernel time
+        "fwd_ms": full["fwd_ms"],
+        "bwd_ms": full["bwd_ms"],
+        "fwd_tflops": full["fwd_tflops"],
+        "bwd_tflops": full["bwd_tflops"],
+        "fwd_frac_peak": full["fwd_frac_peak"],
+        "bwd_frac_peak": full["bwd_frac_peak"],
+        "tail_skip": skip,
+        "fwd_inference_ms": on["coalibi_fwd_kernel (inference)"]["ms"],
+        "ref_convention_tflops": {"fwd": round(2 * fwd_flops / (full["fwd_ms"] * 1e-3) / 1e12, 2),
+                                  "bwd": round(4 * fwd_flops / (full["bwd_ms"] * 1e-3) / 1e12, 2)},
+        "backward_path": head["backward_path"],
+        "kernels": on,
+        "kernels_full_work": head["kernels_full_work"],
         "mfma_ceiling": {"probe_fp16_tflops": round(probe_tflops, 1), "clock_ghz": round(clock_ghz, 3)},
         "sdpa_ms_per_step": None if sdpa_ms is None else round(sdpa_ms, 4),
         "sdpa_mode": sdpa_mode,
         "coalibi_over_sdpa": None if sdpa_ms is None else round(ms_step / sdpa_ms, 3),
-        "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(achieved / peak, 4),
-                     "traffic": None if traffic is None else round(traffic),
-                     # the same kernel's measured HBM rate (traffic over its median time) against
-                     # the 8 TB/s peak: the score-store path moves its records through HBM
-                     "hbm_frac": None if traffic is None else
-                     round(traffic / (per_kernel[dominant]["ms"] * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)},
+        "roofline": roof,
     }
+    if args.configs and w.name == "headline":
+        for name in ("gqa", "long"):
+            r = attention_measure(WORKLOADS[name], args, dev, detail=False)
+            r.pop("_ks")
+            torch.cuda.empty_cache()
+            out[name] = r
+        out["gpt"] = gpt_measure(max(args.steps // 5, 10), max(args.warmup // 5, 5))
     if args.decode:
         out["decode"] = decode_bench(args)
     if args.cpu_seconds > 0:
@@ -391,6 +465,41 @@ def main():
         out["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
         out["cpu_config0_ms"] = round(cpu_config_timing(), 3)
     print(json.dumps(out), flush=True)
+
+
+def sdpa_measure(w, args, dev):
+    """Plain causal attention at the same shape and dtype (torch SDPA on ROCm), fwd + bwd: the cost of
+    Co-ALiBi relative to ordinary attention.  Grouped heads go in with enable_gqa; where that path is
+    unavailable, K and V are expanded to the query heads outside the timed region."""
+    import torch
+    import torch.nn.functional as F
+
+    from co_alibi_attn.workloads import make_inputs
+
+    q, k, v, do = make_inputs(w, seed=0, device=dev)
+    qs, ks_, vs = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    gqa = w.heads_q != w.heads_kv
+
+    def sdpa_step(kk, vv, **kw):
+        qs.grad = ks_.grad = vs.grad = None
+        F.scaled_dot_product_attention(qs, kk, vv, is_causal=w.causal, **kw).backward(do)
+
+    run = lambda: sdpa_step(ks_, vs)  # noqa: E731
+    mode = "mha"
+    if gqa:
+        try:
+            sdpa_step(ks_, vs, enable_gqa=True)
+            run = lambda: sdpa_step(ks_, vs, enable_gqa=True)  # noqa: E731
+            mode = "enable_gqa"
+        except RuntimeError:
+            g = w.heads_q // w.heads_kv
+            kx = ks_.detach().repeat_interleave(g, dim=1).requires_grad_(True)
+            vx = vs.detach().repeat_interleave(g, dim=1).requires_grad_(True)
+            run = lambda: sdpa_step(kx, vx)  # noqa: E731
+            mode = "expanded kv"
+    ms = time_steps(run, args.steps, 3)
+    print(f"[bench] torch SDPA causal fwd+bwd ({mode}): {ms:.3f} ms/step", file=sys.stderr, flush=True)
+    return ms, mode
 
 
 if __name__ == "__main__":

@@ -16,12 +16,16 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 
+ABI_VERSION = 6
+
 # Size of the library-held split-K scratch of co_alibi_decode_noalloc (CO_ALIBI_DECODE_SCRATCH_BYTES).
 DECODE_SCRATCH_BYTES = 32 << 20
 
 # Symbols declared in include/co_alibi.h.
 EXPORTS = (
-    "co_alibi_zb_numel",
+    "co_alibi_stats_numel",
+    "co_alibi_set_tail_skip",
+    "co_alibi_tail_skip",
     "co_alibi_bwd_workspace_bytes",
     "co_alibi_bwd_score_store_workspace_bytes",
     "co_alibi_fwd",
@@ -44,7 +48,9 @@ _F = ctypes.c_float
 _Z = ctypes.c_size_t
 
 _SIGNATURES = {
-    "co_alibi_zb_numel": (_Z, [_I, _I, _I, _I]),
+    "co_alibi_stats_numel": (_Z, [_I, _I, _I, _I]),
+    "co_alibi_set_tail_skip": (_I, [_I]),
+    "co_alibi_tail_skip": (_I, []),
     "co_alibi_bwd_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "co_alibi_bwd_score_store_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I, _I]),
     "co_alibi_fwd": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
@@ -86,7 +92,7 @@ def lib() -> ctypes.CDLL:
         # The version first: a library of another ABI may lack some of the symbols below.
         handle.co_alibi_abi_version.restype = ctypes.c_int
         handle.co_alibi_abi_version.argtypes = []
-        if handle.co_alibi_abi_version() != 5:
+        if handle.co_alibi_abi_version() != ABI_VERSION:
             raise RuntimeError("co_alibi_attn: native library ABI version mismatch; "
                                "run `python -m co_alibi_attn._build`")
         for name, (res, args) in _SIGNATURES.items():
@@ -95,6 +101,24 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = handle
     return _lib
+
+
+class tail_skip:
+    """Context manager over the library's tail-skip setting (co_alibi_set_tail_skip): within
+    ``with tail_skip(False):`` every forward processes every key, as the reference does; the
+    previous setting comes back on exit."""
+
+    def __init__(self, enabled: bool):
+        self.enabled = bool(enabled)
+        self.prev = None
+
+    def __enter__(self):
+        self.prev = lib().co_alibi_set_tail_skip(int(self.enabled))
+        return self
+
+    def __exit__(self, *exc):
+        lib().co_alibi_set_tail_skip(self.prev)
+        return False
 
 
 def check(rc: int) -> None:

@@ -92,16 +92,16 @@ class CoALIBIAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, slopes, causal, sm_scale):
         _check_inputs(q, k, v, slopes)
-        o, lse, zb = ops.fwd(q, k, v, slopes, bool(causal), float(sm_scale), True)
-        ctx.save_for_backward(q, k, v, o, lse, zb, slopes)
+        o, lse, stats = ops.fwd(q, k, v, slopes, bool(causal), float(sm_scale), True)
+        ctx.save_for_backward(q, k, v, o, lse, stats, slopes)
         ctx.sm_scale = float(sm_scale)
         ctx.causal = bool(causal)
         return o
 
     @staticmethod
     def backward(ctx, do):
-        q, k, v, o, lse, zb, slopes = ctx.saved_tensors
-        dq, dk, dv = ops.backward_for(ctx.needs_input_grad, do, q, k, v, o, lse, zb, slopes, ctx.causal,
+        q, k, v, o, lse, stats, slopes = ctx.saved_tensors
+        dq, dk, dv = ops.backward_for(ctx.needs_input_grad, do, q, k, v, o, lse, stats, slopes, ctx.causal,
                                       ctx.sm_scale)
         return dq, dk, dv, None, None, None
 

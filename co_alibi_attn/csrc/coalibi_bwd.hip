@@ -15,18 +15,24 @@
 //
 // C and z couple every key of a row, so the backward runs in two passes that
 // need no atomics and no per-query-block partial buffers:
-//   pass 1 (query-major, keys left to right): S^T, dS^T, dP, dQ^T += K^T dP^T.
-//     It writes D_i and cb[i][J] = sum over keys k < 32J of dA_ik.
+//   pass 1 (query-major, keys left to right from the forward's first processed key):
+//     S^T, dS^T, dP, dQ^T += K^T dP^T.  C is the running prefix carry.  z at each 32-key
+//     block start is rebuilt from the row's sigmoid total R (saved by the forward, O(S)):
+//     z = R minus the sigma totals of the blocks already passed, in fp64.  Each block total
+//     is bitwise the one the forward added into R (the same sigmoids, the same order), so z
+//     is exact up to its final rounding however large R is, and equal wherever the forward
+//     stopped (with or without the tail skip).  Pass 1 writes D_i and, for the recompute
+//     path, zb[J][i] (z at the block start) and cb[J][i] (sum of dA over keys before it)
+//     into the backward's workspace; for the score-store path, the records.
 //   pass 2 (key-major, one work-group per block of keys of a key head): for every
-//     query head of the group and every query tile, S^T, dS^T, dP from the
-//     forward's zb and pass 1's cb, then dV^T += dO^T s and dK^T += Q^T dP.
-//     fp16/bf16: 64 keys per work-group, a wavefront pair per 32-key group that
-//     splits the query tile for S^T/dS^T/dP and the head dim for dV/dK; fp32:
-//     128 keys, one wavefront per 32-key group.
+//     query head of the group and every query tile, dV^T += dO^T s and dK^T += Q^T dP,
+//     from the score store, or recomputing S^T, dS^T and dP from zb and cb.  Recompute
+//     path, fp16/bf16: 64 keys per work-group, a wavefront pair per 32-key group that
+//     splits the query tile for S^T/dS^T/dP and the head dim for dV/dK; fp32: 128 keys,
+//     one wavefront per 32-key group.
 // Both passes hold keys on the accumulator rows (each lane: 16 consecutive keys
 // of one query), so both key scans stay in registers.  z inside a 32-key block
-// is zb[i][J] minus the exclusive prefix of sigma in the block, so no long
-// running sum is ever subtracted from.
+// is zb[i][J] minus the exclusive prefix of sigma in the block.
 // Operands whose reduction runs over LDS rows (K^T in pass 1; Q^T, dO^T, s, dP
 // in pass 2) are read with ds_read_b64_tr_b16 from row-major tiles; the fp32
 // validation mode stores transposed copies instead.
@@ -72,32 +78,35 @@ __device__ __forceinline__ bool pair_ok(int key, int row, int Skv, int Sq, bool 
 // log2 units; sc2 = 1 when an operand carries the scale), dacc = dO.v - D (the dS
 // accumulator starts at -D = -dO.O), zb = sum of sigma over keys >= the block start,
 // cb = sum of dA over keys before the block, lse2 = LSE*log2(e).  Outputs the 16
-// values of s and dP packed for the next products; returns the block's dA total in
-// `atot_blk`.  C is carried multiplied by the slope (lam*C), which makes
+// values of s and dP packed for the next products; returns the block's dA and sigma totals
+// in `atot_blk` and `ztot_blk` (the same value in both halves of the wavefront).  C is carried multiplied by the slope (lam*C), which makes
 // dP = dA - lam*sigma'*C one fma per key after sigma' = sigma - sigma^2.
 template <typename T, bool MASKED, bool CAUSAL>
 __device__ __forceinline__ void dp_tile(const f32x16& sacc, f32x16& dacc, float zb, float cb, float lse2,
                                         int key0, int row, int hh, int Skv, int Sq, float sc2, float lam,
                                         float lam2, typename Mfma<T>::vec8 (&sb)[2],
-                                        typename Mfma<T>::vec8 (&pb)[2], float& atot_blk) {
+                                        typename Mfma<T>::vec8 (&pb)[2], float& atot_blk, float& ztot_blk) {
   using M = Mfma<T>;
-  // Phase 1: sigma, its running (exclusive) prefix over this run folded into
-  // e = t + lam2*prefix, and the run's sigma total.
+  // Phase 1: sigma, its inclusive suffix over this run folded into ex = t - lam2*suffix, and
+  // the run's sigma total, summed from the run's last key down as the forward sums it.
   float sg[16], ex[16];
-  float tot = 0.f;
+  float suf = 0.f;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
+  for (int r = 15; r >= 0; --r) {
     const float t = sacc[r] * sc2;
     float s = sigmoid_log2(t);
     if (MASKED) s = pair_ok(key0 + r, row, Skv, Sq, CAUSAL) ? s : 0.f;
     sg[r] = s;
-    ex[r] = fmaf(lam2, tot, t);
-    tot += s;
+    suf += s;
+    ex[r] = fmaf(-lam2, suf, t);
   }
-  // z = zb - (sigma of the other half's run if it is left of ours) - exclusive prefix, so
-  // log2 of s = t - lam2*z - lse2 = e - (lam2*zbase + lse2).
+  // z = zb - (sigma of the other half's run if it is left of ours) - exclusive prefix, and the
+  // exclusive prefix is the run total minus the inclusive suffix, so
+  // log2 of s = t - lam2*z - lse2 = ex - (lam2*(zb - other - total) + lse2).
+  const float tot = suf;
   const float oth = other_half(tot);
-  const float zbase = zb - (hh ? oth : 0.f);
+  ztot_blk = tot + oth;
+  const float zbase = (zb - (hh ? oth : 0.f)) - tot;
   const float cst = fmaf(lam2, zbase, lse2);
   float atot = 0.f;
   f32x8 sv[2];
@@ -134,7 +143,7 @@ __device__ __forceinline__ void dp_tile(const f32x16& sacc, f32x16& dacc, float 
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1: dQ, D, and cb (recompute path) or the score store (STORE).  Per wavefront 32
+// Pass 1: dQ, D, and zb / cb (recompute path) or the score store (STORE).  Per wavefront 32
 // query rows; register r of lane (col, hh) <-> key k0 + hh*16 + r.
 template <typename T, int D, bool CAUSAL, bool STORE>
 __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coalibi_bwd_dq_kernel(BwdArgs args) {
@@ -155,8 +164,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const int col = lane & 31, hh = lane >> 5;
   const int Sq = args.Sq, Skv = args.Skv;
   const int nQB = (Sq + kBM - 1) / kBM;
-  const WorkItem item = args.row_order ? table_item(args.row_order, blockIdx.x, args.B * args.Hq, gridDim.x)
-                                       : lpt_item(blockIdx.x, args.B * args.Hq, 1);
+  const bool sorted = args.row_order != nullptr && (args.flags[0] & kFlagRowOrder) != 0;
+  const WorkItem item = sorted ? table_item(args.row_order, blockIdx.x, args.B * args.Hq, gridDim.x)
+                               : lpt_item(blockIdx.x, args.B * args.Hq, 1);
   const int bh = item.head;
   const int qb = nQB - 1 - item.rank;  // rank 0: the longest causal rows
   const int b = bh / args.Hq, hq = bh - b * args.Hq;
@@ -181,15 +191,17 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const int last_key = CAUSAL ? min(q0 + kBM - 1, Skv - 1) : Skv - 1;
   const int nkt = last_key / kBN + 1;
   // Keys left of the forward's first processed key are skipped (their dA and dP are below
-  // 2^-T of the row's scale, coalibi_kernels.h); the prefix C starts at zero there.
+  // 2^-T of the row's scale, coalibi_kernels.h); the prefix C starts at zero there.  A kstart
+  // past the block's last tile leaves no tile to process.
   static_assert(kBM == kSkipRows, "kstart entries are per pass-1 row block");
-  const int kt0 = args.kstart[(size_t)bh * nQB + qb] / kBN;
+  const int kt0 = valid_kstart(args.kstart[(size_t)bh * nQB + qb], Skv) / kBN;
 
   // The reads before the first tile go out together and share one round trip: the Q / dO / O
-  // fragments and the lse through buffer resources over the block's valid rows (rows past Sq
-  // read as zero), then the first K / V tile (its address waits only for kstart).
+  // fragments, the lse and the row's sigmoid total through buffer resources over the block's
+  // valid rows (rows past Sq read as zero), then the first K / V tile (its address waits only
+  // for kstart).
   vec8 qf[C::KS], dof[C::KS], of[C::KS];
-  float lse2;
+  float lse2, zhi, zlo;
   {
     const int rows = min(Sq - q0, kBM);
     const size_t blk = qoff + (size_t)q0 * D;
@@ -206,6 +218,11 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     }
     const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(args.lse + (size_t)bh * Sq + q0, rows);
     lse2 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (wave * 32 + col) * 4, 0, 0)) * kLog2e;
+    const size_t nrows = (size_t)args.B * args.Hq * Sq;
+    const __amdgpu_buffer_rsrc_t hrs = tile_rsrc(args.rsum + (size_t)bh * Sq + q0, rows);
+    const __amdgpu_buffer_rsrc_t lors = tile_rsrc(args.rsum + nrows + (size_t)bh * Sq + q0, rows);
+    zhi = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(hrs, (wave * 32 + col) * 4, 0, 0));
+    zlo = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lors, (wave * 32 + col) * 4, 0, 0));
   }
   float dpart = 0.f;
   // fp32 folds dO.O before the tile loads: holding O across them spills.
@@ -234,26 +251,20 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
   float crun = 0.f;
-  const float* __restrict__ zb_row = args.zb + (size_t)bh * args.nZB * Sq + row;
+  // z at the next block start: R minus the sigma totals of the blocks passed, in fp64.
+  double zsum = (double)zhi + (double)zlo;
+  float* __restrict__ zb_row = STORE ? nullptr : args.zb + (size_t)bh * args.nZB * Sq + row;
   float* __restrict__ cb_row = STORE ? nullptr : args.cb + (size_t)bh * args.nZB * Sq + row;
   const int nQ32 = (Sq + 31) / 32;
 
   // The memory counter completes in order and counts stores: a wait for a load also waits for
   // every store issued before it, and where paths meet the compiler waits for the shortest
   // count of any path.  So that the score-store records drain under the next tiles' work:
-  //  - each tile's zb is loaded during the tile before it, ahead of that tile's stores, into the
-  //    same register (a copy between registers would wait for the load);
   //  - the K/V staging uses barriers that wait for LDS only (__syncthreads waits for the stores);
-  //  - the K/V and zb loads and the record stores are buffer operations issued on every path,
-  //    their ranges covering only what exists (the rest reads as zero or is dropped);
+  //  - the K/V loads and the record stores are buffer operations issued on every path, their
+  //    ranges covering only what exists (the rest reads as zero or is dropped);
   //  - the tiles that some wavefront skips (causal: the last ones) run in a loop of their own,
   //    so the skip is not a path of the main loop.
-  auto load_zb = [&](int t) {  // this row's zb of tile t; zero past Sq and for t >= nkt
-    const int n = t < nkt ? max(min(Sq - wrow0, 32), 0) : 0;
-    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(args.zb + ((size_t)bh * args.nZB + t) * Sq + wrow0, n);
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, col * 4, 0, 0));
-  };
-  float zb = load_zb(kt0);
   auto tile = [&](int kt, auto tail) __attribute__((always_inline)) {
     lds_barrier();  // every wavefront's reads of the previous tile are done
     kregs.store_rows(sK, C::LDR, tid);
@@ -283,19 +294,22 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     }
     __builtin_amdgcn_sched_barrier(0);
     vec8 sb[2], pb[2];
-    float atot;
+    float atot, ztot;
+    const float zb = (float)zsum;
     if (masked)
       dp_tile<T, true, CAUSAL>(sacc, dacc, zb, crun, lse2, k0 + hh * 16, row, hh, Skv, Sq, tile_sc2, lam, lam2,
-                               sb, pb, atot);
+                               sb, pb, atot, ztot);
     else
       dp_tile<T, false, CAUSAL>(sacc, dacc, zb, crun, lse2, k0 + hh * 16, row, hh, Skv, Sq, tile_sc2, lam, lam2,
-                                sb, pb, atot);
-    zb = load_zb(kt + 1);           // the next tile's (above)
-    asm volatile("" ::: "memory");  // issued here, before the tile's stores
+                                sb, pb, atot, ztot);
     if constexpr (!STORE) {
-      if (hh == 0 && row_ok) cb_row[(size_t)kt * Sq] = crun;
+      if (hh == 0 && row_ok) {
+        zb_row[(size_t)kt * Sq] = zb;
+        cb_row[(size_t)kt * Sq] = crun;
+      }
     }
     crun += atot;
+    zsum -= (double)ztot;
     __builtin_amdgcn_sched_barrier(0);
     // dQ^T[d][q] += K^T[d][key] dP^T[key][q];  A rows are keys hh*16 + mh*8 + e.
 #pragma unroll
@@ -485,8 +499,8 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
     if (w + 1 < nwork) prefetch(w + 1);
     if (kw0 >= Skv) continue;
     // This wavefront's 32 keys lie left of the forward's first processed key for the
-    // tile's row block (a multiple of 64): skipped, with no zb written for them.
-    if (kw0 < args.kstart[(size_t)(b * args.Hq + hq) * nSkipQB + (q0 / kSkipRows)]) continue;
+    // tile's row block (a multiple of 64): skipped, as pass 1 skipped them (no zb written).
+    if (kw0 < valid_kstart(args.kstart[(size_t)(b * args.Hq + hq) * nSkipQB + (q0 / kSkipRows)], Skv)) continue;
 #pragma unroll
     for (int sq = 0; sq < BQ / 32; ++sq) {
       const int qs0 = q0 + sq * 32;
@@ -506,13 +520,13 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
       }
       __builtin_amdgcn_sched_barrier(0);
       vec8 sb[2], pb[2];
-      float atot;
+      float atot, ztot;
       if (masked)
         dp_tile<T, true, CAUSAL>(sacc, dacc, sZb[wave][ql], sCb[wave][ql], sLse2[ql], key0, row, hh, Skv, Sq,
-                                 tile_sc2, lam, lam2, sb, pb, atot);
+                                 tile_sc2, lam, lam2, sb, pb, atot, ztot);
       else
         dp_tile<T, false, CAUSAL>(sacc, dacc, sZb[wave][ql], sCb[wave][ql], sLse2[ql], key0, row, hh, Skv, Sq,
-                                  tile_sc2, lam, lam2, sb, pb, atot);
+                                  tile_sc2, lam, lam2, sb, pb, atot, ztot);
       // s and dP to this wavefront's scratch, then back as operands reduced over queries.
       if constexpr (C::kTr) {
         *reinterpret_cast<vec8*>(sS + col * C::LDSP + hh * 16) = sb[0];
@@ -622,7 +636,8 @@ struct KeyBlockWork {
 // the caller synchronises before reading it.  BQ rows per tile, two tiles per kstart entry.
 template <int BQ>
 __device__ __forceinline__ KeyBlockWork key_block_work(int* qthi, const int* __restrict__ kstart_g, int group,
-                                                       int Sq, int qt0, int kwg0, int wave, int nwaves, int lane) {
+                                                       int Sq, int Skv, int qt0, int kwg0, int wave, int nwaves,
+                                                       int lane) {
   static_assert(BQ * 2 == kSkipRows, "two query tiles per kstart row block");
   const int nQT = (Sq + BQ - 1) / BQ;
   const int nSkipQB = (Sq + kSkipRows - 1) / kSkipRows;
@@ -631,7 +646,7 @@ __device__ __forceinline__ KeyBlockWork key_block_work(int* qthi, const int* __r
     for (int g = wave; g < group; g += nwaves) {
       int hi = qt0 - 1;
       for (int rb = lane; rb < nSkipQB; rb += 64)
-        if (kstart_g[(size_t)g * nSkipQB + rb] <= kwg0) hi = max(hi, min(2 * rb + 1, nQT - 1));
+        if (valid_kstart(kstart_g[(size_t)g * nSkipQB + rb], Skv) <= kwg0) hi = max(hi, min(2 * rb + 1, nQT - 1));
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) hi = max(hi, __shfl_xor(hi, off));
       if (lane == 0) qthi[g] = hi;
@@ -671,9 +686,10 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   const int kg = wave >> 1, qh = wave & 1;
   const int Sq = args.Sq, Skv = args.Skv;
   static_assert(sizeof(sSP) >= 2 * kMaxBalancedHeads * 4, "the head order is built in sSP");
+  const bool sorted = args.key_order != nullptr && (args.flags[0] & kFlagKeyOrder) != 0;
   const WorkItem item =
-      args.key_order ? table_item(args.key_order, blockIdx.x, args.B * args.Hkv, gridDim.x)
-                     : balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
+      sorted ? table_item(args.key_order, blockIdx.x, args.B * args.Hkv, gridDim.x)
+             : balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
                                      reinterpret_cast<float*>(&sSP[0][0][0]),
                                      reinterpret_cast<int*>(&sSP[0][0][0]) + kMaxBalancedHeads, tid, 64 * kPairWaves);
   const int bhk = item.head;               // b * Hkv + hkv
@@ -726,7 +742,7 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
   const int kwg0 = kb * kPairBK;
   const int* __restrict__ kstart_g = args.kstart + (size_t)(b * args.Hq + hkv * group) * nSkipQB;
   const KeyBlockWork work =
-      key_block_work<BQ>(sQtHi, kstart_g, group, Sq, qt0, kwg0, wave, kPairWaves, lane);
+      key_block_work<BQ>(sQtHi, kstart_g, group, Sq, Skv, qt0, kwg0, wave, kPairWaves, lane);
   // K pre-scaled by sm_scale*log2(e), so S^T comes out in log2 units.
 #pragma unroll
   for (int ks = 0; ks < C::KS; ++ks) ka[ks] = scale_vec8<T>(ka[ks], args.sc2);
@@ -791,7 +807,7 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
 
     // Query half h of the tile meets this key group (some pair is visible) and the
     // forward processed these keys for the tile's row block.
-    const bool processed = kwg0 >= kstart_g[(size_t)gi * nSkipQB + qt / 2];
+    const bool processed = kwg0 >= valid_kstart(kstart_g[(size_t)gi * nSkipQB + qt / 2], Skv);
     auto half_live = [&](int h) {
       const int qs0 = q0 + h * 32;
       return processed && keys_ok && qs0 < Sq && (!CAUSAL || qs0 + 31 >= kw0);
@@ -812,13 +828,13 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
                       dacc);
       }
       vec8 sb[2], pb[2];
-      float atot;
+      float atot, ztot;
       if (masked)
         dp_tile<T, true, CAUSAL>(sacc, dacc, sZb[buf][kg][ql], sCb[buf][kg][ql], sLse2[buf][ql], key0, row, hh,
-                                 Skv, Sq, 1.0f, lam, lam2, sb, pb, atot);
+                                 Skv, Sq, 1.0f, lam, lam2, sb, pb, atot, ztot);
       else
         dp_tile<T, false, CAUSAL>(sacc, dacc, sZb[buf][kg][ql], sCb[buf][kg][ql], sLse2[buf][ql], key0, row, hh,
-                                  Skv, Sq, 1.0f, lam, lam2, sb, pb, atot);
+                                  Skv, Sq, 1.0f, lam, lam2, sb, pb, atot, ztot);
       *reinterpret_cast<vec8*>(sS + ql * LDSP + hh * 16) = sb[0];
       *reinterpret_cast<vec8*>(sS + ql * LDSP + hh * 16 + 8) = sb[1];
       *reinterpret_cast<vec8*>(sP + ql * LDSP + hh * 16) = pb[0];
@@ -914,10 +930,11 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
   const int kg = wave >> 1, qh = wave & 1;
   const int Sq = args.Sq, Skv = args.Skv;
   static_assert(sizeof(sQ[1]) >= 2 * kMaxBalancedHeads * 4, "the head order is built in sQ[1]");
-  const WorkItem item = args.key_order ? table_item(args.key_order, blockIdx.x, args.B * args.Hkv, gridDim.x)
-                                       : balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
-                                                       reinterpret_cast<float*>(sQ[1]),
-                                                       reinterpret_cast<int*>(sQ[1]) + kMaxBalancedHeads, tid, 256);
+  const bool sorted = args.key_order != nullptr && (args.flags[0] & kFlagKeyOrder) != 0;
+  const WorkItem item = sorted ? table_item(args.key_order, blockIdx.x, args.B * args.Hkv, gridDim.x)
+                               : balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
+                                               reinterpret_cast<float*>(sQ[1]),
+                                               reinterpret_cast<int*>(sQ[1]) + kMaxBalancedHeads, tid, 256);
   const int bhk = item.head;  // b * Hkv + hkv
   const int kb = item.rank;   // rank 0: key block 0, seen by the most query rows
   const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;
@@ -932,12 +949,13 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
   const int qt0 = CAUSAL ? min(kwg0 / BQ, nQT) : 0;
   const int nSkipQB = (Sq + kSkipRows - 1) / kSkipRows;
   const int* __restrict__ kstart_g = args.kstart + (size_t)(b * args.Hq + hkv * group) * nSkipQB;
-  const KeyBlockWork work = key_block_work<BQ>(sQtHi, kstart_g, group, Sq, qt0, kwg0, wave, 4, lane);
+  const KeyBlockWork work = key_block_work<BQ>(sQtHi, kstart_g, group, Sq, Skv, qt0, kwg0, wave, 4, lane);
   const int wph = (nSkipQB + 63) / 64 * 2;  // words per head (the host checks group * wph fits)
   for (int g = wave; g < group; g += 4) {
     for (int rb0 = 0; rb0 < nSkipQB; rb0 += 64) {
       const int rb = rb0 + lane;
-      const unsigned long long m = __ballot(rb < nSkipQB && kstart_g[(size_t)g * nSkipQB + rb] <= kwg0);
+      const unsigned long long m =
+          __ballot(rb < nSkipQB && valid_kstart(kstart_g[(size_t)g * nSkipQB + rb], Skv) <= kwg0);
       if (lane == 0) {
         sProc[g * wph + rb0 / 32] = static_cast<unsigned>(m);
         sProc[g * wph + rb0 / 32 + 1] = static_cast<unsigned>(m >> 32);
@@ -1066,7 +1084,7 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream) {
   // The score-store path (BwdArgs::scores set by the caller for the types and head dims
-  // that have it) replaces cb with the records and pass 2 with the store kernel.
+  // that have it) replaces zb / cb with the records and pass 2 with the store kernel.
   constexpr bool kStore = sizeof(T) == 2 && (D == 64 || D == 128);
   const bool store = kStore && a.scores != nullptr;
   static_assert(kStoreBK == kOrderKeyBlock && kPairBK == kOrderKeyBlock, "key_order numbers 64-key blocks");

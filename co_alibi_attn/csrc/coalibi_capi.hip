@@ -25,9 +25,28 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 size_t num_zblocks(int seq_kv) { return (static_cast<size_t>(seq_kv) + 31) / 32; }
 
-// fp32 elements of the zb blocks proper, before the kstart / knorm tails.
-size_t zb_block_numel(int batch, int heads_q, int seq_q, int seq_kv) {
+// fp32 elements of one per-32-key-block array of the recompute path's workspace (zb or cb).
+size_t block_sums_numel(int batch, int heads_q, int seq_q, int seq_kv) {
   return static_cast<size_t>(batch) * heads_q * num_zblocks(seq_kv) * seq_q;
+}
+
+// The tail skip (the library setting of co_alibi_set_tail_skip): on unless switched off.
+std::atomic<int> g_tail_skip{1};
+
+// Where the parts of the forward's statistics lie (coalibi_kernels.h).
+struct StatsLayout {
+  size_t kstart, knorm, row_order, key_order, rsum, total;  // offsets in 4-byte words
+};
+StatsLayout stats_layout(int batch, int heads_q, int seq_q, int seq_kv) {
+  const size_t bh = static_cast<size_t>(batch) * heads_q;
+  StatsLayout l;
+  l.kstart = coalibi::kStatsHeader;
+  l.knorm = l.kstart + bh * coalibi::stats_kstart_count(seq_q);
+  l.row_order = l.knorm + bh * coalibi::stats_knorm_count(seq_kv);
+  l.key_order = l.row_order + bh * coalibi::stats_kstart_count(seq_q);
+  l.rsum = l.key_order + bh * coalibi::stats_key_block_count(seq_kv);
+  l.total = l.rsum + 2 * bh * static_cast<size_t>(seq_q);
+  return l;
 }
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -111,19 +130,21 @@ hipError_t bwd_dispatch_d(const coalibi::BwdArgs& a, int D, bool causal, int sta
 
 extern "C" {
 
-size_t co_alibi_zb_numel(int batch, int heads_q, int seq_q, int seq_kv) {
+size_t co_alibi_stats_numel(int batch, int heads_q, int seq_q, int seq_kv) {
   if (batch < 1 || heads_q < 1 || seq_q < 1 || seq_kv < 1) return 0;
-  return zb_block_numel(batch, heads_q, seq_q, seq_kv) +
-         static_cast<size_t>(batch) * heads_q *
-             (2 * coalibi::zb_kstart_count(seq_q) + coalibi::zb_knorm_count(seq_kv) +
-              coalibi::zb_key_block_count(seq_kv));
+  return stats_layout(batch, heads_q, seq_q, seq_kv).total;
 }
 
 size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_kv) {
   if (batch < 1 || heads_q < 1 || seq_q < 1 || seq_kv < 1) return 0;
   const size_t rows = static_cast<size_t>(batch) * heads_q * seq_q;
-  return round_up(rows * sizeof(float), 256) + zb_block_numel(batch, heads_q, seq_q, seq_kv) * sizeof(float);
+  return round_up(rows * sizeof(float), 256) +
+         2 * round_up(block_sums_numel(batch, heads_q, seq_q, seq_kv) * sizeof(float), 256);
 }
+
+int co_alibi_set_tail_skip(int enabled) { return g_tail_skip.exchange(enabled != 0 ? 1 : 0); }
+
+int co_alibi_tail_skip(void) { return g_tail_skip.load(); }
 
 size_t co_alibi_bwd_score_store_workspace_bytes(int dtype, int batch, int heads_q, int heads_kv, int seq_q,
                                                 int seq_kv, int head_dim, int causal) {
@@ -139,7 +160,7 @@ size_t co_alibi_bwd_score_store_workspace_bytes(int dtype, int batch, int heads_
 size_t co_alibi_fwd_inference_workspace_bytes(int batch, int heads_q, int seq_q, int seq_kv) {
   if (batch < 1 || heads_q < 1 || seq_q < 1 || seq_kv < 1) return 0;
   return round_up(static_cast<size_t>(batch) * heads_q *
-                      (coalibi::zb_knorm_count(seq_kv) + coalibi::zb_kstart_count(seq_q)) * sizeof(float),
+                      (coalibi::stats_knorm_count(seq_kv) + coalibi::stats_kstart_count(seq_q)) * sizeof(float),
                   256);
 }
 
@@ -147,18 +168,19 @@ size_t co_alibi_fwd_inference_workspace_bytes(int batch, int heads_q, int seq_q,
 
 namespace {
 
-// The forward with its statistics (lse, zb with the kstart / knorm tails), without them
-// (lse = zb = NULL: no tail skip), or for inference (knorm scratch only: the tail skip
-// without the backward's statistics).
+// The forward with its statistics (lse and stats: kstart, the key norms and the work orders),
+// without them (lse = stats = NULL: no tail skip), or for inference (knorm scratch only: the
+// tail skip without the backward's statistics).  With the tail skip switched off
+// (co_alibi_set_tail_skip) no key norms are computed and every key is processed.
 int fwd_impl(const char* fn, int dtype, const void* q, const void* k, const void* v, const float* slopes, void* o,
-             float* lse, float* zb, float* knorm_ws, int batch, int heads_q, int heads_kv, int seq_q, int seq_kv,
-             int head_dim, int causal, float sm_scale, void* stream) {
+             float* lse, float* stats, float* knorm_ws, int batch, int heads_q, int heads_kv, int seq_q,
+             int seq_kv, int head_dim, int causal, float sm_scale, void* stream) {
   const Shape s{batch, heads_q, heads_kv, seq_q, seq_kv, head_dim};
   int rc;
   if ((rc = check_shape(fn, dtype, s))) return rc;
   if ((rc = check_ptr(fn, "q", q, 16)) || (rc = check_ptr(fn, "k", k, 16)) || (rc = check_ptr(fn, "v", v, 16)) ||
       (rc = check_ptr(fn, "o", o, 16)) || (rc = check_ptr(fn, "slopes", slopes, 4)) ||
-      (rc = check_opt_ptr(fn, "lse", lse, 4)) || (rc = check_opt_ptr(fn, "zb", zb, 4)))
+      (rc = check_opt_ptr(fn, "lse", lse, 4)) || (rc = check_opt_ptr(fn, "stats", stats, 4)))
     return rc;
   if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": sm_scale must be finite");
 
@@ -169,27 +191,29 @@ int fwd_impl(const char* fn, int dtype, const void* q, const void* k, const void
   a.slopes = slopes;
   a.o = o;
   a.lse = lse;
-  a.zb = zb;
-  const size_t bh = static_cast<size_t>(batch) * heads_q;
-  if (zb != nullptr) {  // kstart, knorm and the work orders follow the zb blocks (coalibi_kernels.h)
-    float* tail = zb + zb_block_numel(batch, heads_q, seq_q, seq_kv);
-    a.kstart = reinterpret_cast<int*>(tail);
-    a.knorm = tail + bh * coalibi::zb_kstart_count(seq_q);
-    int* orders = reinterpret_cast<int*>(
-        tail + bh * (coalibi::zb_kstart_count(seq_q) + coalibi::zb_knorm_count(seq_kv)));
-    a.row_order = orders;
-    a.key_order = orders + bh * coalibi::zb_kstart_count(seq_q);
-  } else if (knorm_ws != nullptr) {  // inference: the row order follows the norms
+  const bool skip = g_tail_skip.load() != 0;
+  if (stats != nullptr) {  // header, kstart, knorm and the work orders (coalibi_kernels.h)
+    const StatsLayout l = stats_layout(batch, heads_q, seq_q, seq_kv);
+    int* words = reinterpret_cast<int*>(stats);
+    a.flags = words;
+    a.kstart = words + l.kstart;
+    a.rsum = stats + l.rsum;
+    if (skip) {
+      a.knorm = stats + l.knorm;
+      a.row_order = words + l.row_order;
+      a.key_order = words + l.key_order;
+    }
+  } else if (knorm_ws != nullptr && skip) {  // inference: the row order follows the norms
     a.knorm = knorm_ws;
-    a.row_order = reinterpret_cast<int*>(knorm_ws + bh * coalibi::zb_knorm_count(seq_kv));
+    a.row_order = reinterpret_cast<int*>(knorm_ws + static_cast<size_t>(batch) * heads_q *
+                                                        coalibi::stats_knorm_count(seq_kv));
   }
   a.B = batch;
   a.Hq = heads_q;
   a.Hkv = heads_kv;
   a.Sq = seq_q;
   a.Skv = seq_kv;
-  a.nZB = static_cast<int>(num_zblocks(seq_kv));
-  a.nKC = coalibi::zb_knorm_count(seq_kv);
+  a.nKC = coalibi::stats_knorm_count(seq_kv);
   a.sc2 = sm_scale * coalibi::kLog2eHost;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
@@ -207,9 +231,9 @@ int fwd_impl(const char* fn, int dtype, const void* q, const void* k, const void
 extern "C" {
 
 int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const float* slopes, void* o,
-                 float* lse, float* zb, int batch, int heads_q, int heads_kv, int seq_q, int seq_kv,
+                 float* lse, float* stats, int batch, int heads_q, int heads_kv, int seq_q, int seq_kv,
                  int head_dim, int causal, float sm_scale, void* stream) {
-  return fwd_impl("co_alibi_fwd", dtype, q, k, v, slopes, o, lse, zb, nullptr, batch, heads_q, heads_kv, seq_q,
+  return fwd_impl("co_alibi_fwd", dtype, q, k, v, slopes, o, lse, stats, nullptr, batch, heads_q, heads_kv, seq_q,
                   seq_kv, head_dim, causal, sm_scale, stream);
 }
 
@@ -231,9 +255,9 @@ int co_alibi_fwd_inference(int dtype, const void* q, const void* k, const void* 
 
 namespace {
 
-// stages: 1 = pass 1 (dq, dsum, and cb or the score store), 2 = pass 2 (dk, dv), 3 = both.
+// stages: 1 = pass 1 (dq, dsum, and zb / cb or the score store), 2 = pass 2 (dk, dv), 3 = both.
 int bwd_impl(const char* fn, int stages, int dtype, const void* dout, const void* q, const void* k,
-             const void* v, const void* o, const float* lse, const float* zb, const float* slopes, void* dq,
+             const void* v, const void* o, const float* lse, const float* stats, const float* slopes, void* dq,
              void* dk, void* dv, void* workspace, size_t workspace_bytes, int batch, int heads_q,
              int heads_kv, int seq_q, int seq_kv, int head_dim, int causal, float sm_scale, void* stream) {
   const Shape s{batch, heads_q, heads_kv, seq_q, seq_kv, head_dim};
@@ -241,7 +265,7 @@ int bwd_impl(const char* fn, int stages, int dtype, const void* dout, const void
   if ((rc = check_shape(fn, dtype, s))) return rc;
   if ((rc = check_ptr(fn, "dout", dout, 16)) || (rc = check_ptr(fn, "q", q, 16)) ||
       (rc = check_ptr(fn, "k", k, 16)) || (rc = check_ptr(fn, "v", v, 16)) ||
-      (rc = check_ptr(fn, "lse", lse, 4)) || (rc = check_ptr(fn, "zb", zb, 4)) ||
+      (rc = check_ptr(fn, "lse", lse, 4)) || (rc = check_ptr(fn, "stats", stats, 4)) ||
       (rc = check_ptr(fn, "slopes", slopes, 4)) || (rc = check_ptr(fn, "workspace", workspace, 256)))
     return rc;
   if ((stages & 1) && ((rc = check_ptr(fn, "o", o, 16)) || (rc = check_ptr(fn, "dq", dq, 16)))) return rc;
@@ -264,29 +288,29 @@ int bwd_impl(const char* fn, int stages, int dtype, const void* dout, const void
   a.v = v;
   a.o = o;
   a.lse = lse;
-  a.zb = zb;
   a.slopes = slopes;
   a.dq = dq;
   a.dk = dk;
   a.dv = dv;
   a.dsum = static_cast<float*>(workspace);
   char* const after_dsum = static_cast<char*>(workspace) + round_up(rows * sizeof(float), 256);
-  if (store) {  // the records follow dsum; no cb
+  if (store) {  // the records follow dsum
     a.scores = after_dsum;
     a.score_head = coalibi::score_records_per_head(seq_q, seq_kv, causal != 0);
-  } else {
-    a.cb = reinterpret_cast<float*>(after_dsum);
+  } else {  // zb and cb follow dsum
+    a.zb = reinterpret_cast<float*>(after_dsum);
+    a.cb = reinterpret_cast<float*>(after_dsum +
+                                    round_up(block_sums_numel(batch, heads_q, seq_q, seq_kv) * sizeof(float), 256));
   }
-  {  // the zb tail: kstart, knorm, then the work orders the forward wrote
-    const size_t bh = static_cast<size_t>(batch) * heads_q;
-    const float* tail = zb + zb_block_numel(batch, heads_q, seq_q, seq_kv);
-    a.kstart = reinterpret_cast<const int*>(tail);
-    const int* orders = reinterpret_cast<const int*>(tail + bh * (coalibi::zb_kstart_count(seq_q) +
-                                                                 coalibi::zb_knorm_count(seq_kv)));
-    a.row_order = coalibi::row_order_fits(batch, heads_q, seq_q) ? orders : nullptr;
-    a.key_order = coalibi::key_order_used(batch, heads_q, heads_kv, seq_kv)
-                      ? orders + bh * coalibi::zb_kstart_count(seq_q)
-                      : nullptr;
+  {  // the forward's statistics: header, kstart, knorm, then the work orders it wrote (the
+     // kernels follow a table only where the header's flags say it was written)
+    const StatsLayout l = stats_layout(batch, heads_q, seq_q, seq_kv);
+    const int* words = reinterpret_cast<const int*>(stats);
+    a.flags = words;
+    a.kstart = words + l.kstart;
+    a.rsum = stats + l.rsum;
+    a.row_order = words + l.row_order;
+    a.key_order = coalibi::key_order_used(batch, heads_q, heads_kv, seq_kv) ? words + l.key_order : nullptr;
   }
   a.B = batch;
   a.Hq = heads_q;
@@ -312,27 +336,27 @@ int bwd_impl(const char* fn, int stages, int dtype, const void* dout, const void
 extern "C" {
 
 int co_alibi_bwd(int dtype, const void* dout, const void* q, const void* k, const void* v, const void* o,
-                 const float* lse, const float* zb, const float* slopes, void* dq, void* dk, void* dv,
+                 const float* lse, const float* stats, const float* slopes, void* dq, void* dk, void* dv,
                  void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv, int seq_q,
                  int seq_kv, int head_dim, int causal, float sm_scale, void* stream) {
-  return bwd_impl("co_alibi_bwd", 3, dtype, dout, q, k, v, o, lse, zb, slopes, dq, dk, dv, workspace,
+  return bwd_impl("co_alibi_bwd", 3, dtype, dout, q, k, v, o, lse, stats, slopes, dq, dk, dv, workspace,
                   workspace_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal, sm_scale, stream);
 }
 
 int co_alibi_bwd_dq(int dtype, const void* dout, const void* q, const void* k, const void* v, const void* o,
-                    const float* lse, const float* zb, const float* slopes, void* dq, void* workspace,
+                    const float* lse, const float* stats, const float* slopes, void* dq, void* workspace,
                     size_t workspace_bytes, int batch, int heads_q, int heads_kv, int seq_q, int seq_kv,
                     int head_dim, int causal, float sm_scale, void* stream) {
-  return bwd_impl("co_alibi_bwd_dq", 1, dtype, dout, q, k, v, o, lse, zb, slopes, dq, nullptr, nullptr,
+  return bwd_impl("co_alibi_bwd_dq", 1, dtype, dout, q, k, v, o, lse, stats, slopes, dq, nullptr, nullptr,
                   workspace, workspace_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal,
                   sm_scale, stream);
 }
 
 int co_alibi_bwd_dkdv(int dtype, const void* dout, const void* q, const void* k, const void* v,
-                      const float* lse, const float* zb, const float* slopes, void* dk, void* dv,
+                      const float* lse, const float* stats, const float* slopes, void* dk, void* dv,
                       void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv,
                       int seq_q, int seq_kv, int head_dim, int causal, float sm_scale, void* stream) {
-  return bwd_impl("co_alibi_bwd_dkdv", 2, dtype, dout, q, k, v, nullptr, lse, zb, slopes, nullptr, dk, dv,
+  return bwd_impl("co_alibi_bwd_dkdv", 2, dtype, dout, q, k, v, nullptr, lse, stats, slopes, nullptr, dk, dv,
                   workspace, workspace_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal,
                   sm_scale, stream);
 }
@@ -447,13 +471,8 @@ int decode_impl(const char* fn, bool scratch_ws, int dtype, const void* q, const
   if (decode_chunks(seq_kv) > static_cast<size_t>(coalibi::kMaxDecodeChunks))
     return fail(CO_ALIBI_EINVAL, std::string(fn) + ": seq_kv above " +
                                      std::to_string(coalibi::kMaxDecodeChunks * coalibi::kDecodeChunkKeys));
-  if ((rc = check_ptr(fn, "q", q, 16)) || (rc = check_ptr(fn, "k_cache", k_cache, 16)) ||
-      (rc = check_ptr(fn, "v_cache", v_cache, 16)) || (rc = check_ptr(fn, "o", o, 16)) ||
-      (rc = check_ptr(fn, "slopes", slopes, 4)) || (rc = check_opt_ptr(fn, "seq_lens", seq_lens, 4)) ||
-      (rc = check_opt_ptr(fn, "lse", lse, 4)) || (rc = check_ptr(fn, "workspace", workspace, 256)))
-    return rc;
-  if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": sm_scale must be finite");
-
+  // The workspace size first: it depends on the shape only, and a decode whose partials do not fit
+  // is refused before any pointer is looked at.
   const DecodeSplit sp = decode_split(batch, heads_kv, seq_kv);
   const size_t rows = static_cast<size_t>(batch) * heads_q;
   const size_t parts = rows * (scratch_ws ? static_cast<size_t>(sp.nSplits) : decode_splits_max(seq_kv));
@@ -466,6 +485,12 @@ int decode_impl(const char* fn, bool scratch_ws, int dtype, const void* q, const
     return fail(CO_ALIBI_EINVAL, std::string(fn) + ": workspace of " + std::to_string(workspace_bytes) +
                                      " bytes, need " + std::to_string(need));
   }
+  if ((rc = check_ptr(fn, "q", q, 16)) || (rc = check_ptr(fn, "k_cache", k_cache, 16)) ||
+      (rc = check_ptr(fn, "v_cache", v_cache, 16)) || (rc = check_ptr(fn, "o", o, 16)) ||
+      (rc = check_ptr(fn, "slopes", slopes, 4)) || (rc = check_opt_ptr(fn, "seq_lens", seq_lens, 4)) ||
+      (rc = check_opt_ptr(fn, "lse", lse, 4)) || (rc = check_ptr(fn, "workspace", workspace, 256)))
+    return rc;
+  if (!std::isfinite(sm_scale)) return fail(CO_ALIBI_EINVAL, std::string(fn) + ": sm_scale must be finite");
 
   const size_t stat_bytes = round_up(parts * sizeof(float), 256);
   char* ws = static_cast<char*>(workspace);
@@ -531,6 +556,6 @@ int co_alibi_decode_noalloc(int dtype, const void* q, const void* k_cache, const
 
 const char* co_alibi_last_error(void) { return g_last_error.c_str(); }
 
-int co_alibi_abi_version(void) { return 5; }
+int co_alibi_abi_version(void) { return 6; }
 
 }  // extern "C"

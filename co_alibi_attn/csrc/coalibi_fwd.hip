@@ -19,8 +19,11 @@
 //   O^T += V^T P^T (MFMA, the P accumulators are reused as the B operand).
 // K is staged in LDS row-major (rows permuted); V row-major, read as the
 // transposed operand with ds_read_b64_tr_b16 (fp32 mode: V stored transposed).
-// Besides O and LSE the kernel writes zb: the suffix sum at every 32-key block
-// start, the only penalty statistic the backward needs.
+// Besides O and LSE the kernel saves, per 128-row block, the first key it processed
+// (kstart, the tail skip's record), and per row the sum R of the sigmoids of the keys it
+// processed: backward pass 1 rebuilds z from it.  R is summed in fp64 over 32-key block
+// totals, exactly the totals pass 1 computes (the same sigmoids summed in the same order), so
+// the difference pass 1 takes is exact up to one rounding.
 #include "coalibi_common.h"
 #include "coalibi_kernels.h"
 
@@ -58,13 +61,15 @@ __device__ __forceinline__ bool key_ok(int key, int row, int Skv) {
 
 // One 64-key tile for one wavefront.  State: acc (O^T, scaled by 2^-m2), m2
 // (log2-domain scale, -inf before the first visible key), lsum (this half's
-// share of sum_j 2^(a_j - m2)), zr (sigmoid sum of all keys right of the tile).
+// share of sum_j 2^(a_j - m2)), zr (sigmoid sum of all keys right of the tile, read only).
+// Returns the sigmoid totals of the tile's two 32-key blocks, keys k0 + 32.. in btot[1] and k0..
+// in btot[0] (the same values in both halves of the wavefront).
 template <typename T, int D, bool CAUSAL, bool MASKED>
 __device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __restrict__ sV,
                                          const typename Mfma<T>::vec8 (&qf)[FwdCfg<T, D>::KS],
                                          f32x16 (&acc)[FwdCfg<T, D>::DT], float& m2, float& lsum,
-                                         float& zr, float& zst0, float& zst1, int k0, int row, int lane,
-                                         int Skv, float sc2, float lam2) {
+                                         float zr, float (&btot)[2], int k0, int row, int lane, int Skv,
+                                         float sc2, float lam2) {
   using C = FwdCfg<T, D>;
   using M = Mfma<T>;
   const int col = lane & 31, hh = lane >> 5;
@@ -100,10 +105,10 @@ __device__ __forceinline__ void fwd_tile(const T* __restrict__ sK, const T* __re
   const float oth0 = other_half(tot[0]), oth1 = other_half(tot[1]);
   const float T11 = hh ? tot[1] : oth1, T10 = hh ? oth1 : tot[1];
   const float T01 = hh ? tot[0] : oth0, T00 = hh ? oth0 : tot[0];
-  zst1 = (zr + T11) + T10;    // suffix sum from key k0 + 32
-  zst0 = (zst1 + T01) + T00;  // suffix sum from key k0
+  const float zst1 = (zr + T11) + T10;  // suffix sum from key k0 + 32
   const float off[2] = {hh ? zst1 : zst1 + T01, hh ? zr : zr + T11};
-  zr = zst0;
+  btot[1] = T11 + T10;
+  btot[0] = T01 + T00;
 
   // Log2-domain logit relative to the current scale:
   //   t - lam2 * (off + loc) - mb = fma(-lam2, loc, fma(s, sc2, -(mb + lam2 * off)))
@@ -301,7 +306,7 @@ struct KeyCost {
 };
 
 // Work-group 0 writes the row order, work-group 1 the key order.  Every element of both tables
-// is written (the zb buffer is an output): a table that is not sorted holds its index order,
+// is written (the statistics are an output): a table that is not sorted holds its index order,
 // and the key table's room for B*Hq*nKB entries past its B*Hkv*nKB items holds zeros.
 __device__ void schedule_orders(const ScheduleArgs& s, int which, int tid) {
   __shared__ int lds[5 * kOrderBuckets];
@@ -323,7 +328,7 @@ __device__ void schedule_orders(const ScheduleArgs& s, int which, int tid) {
       for (int i = tid; i < n; i += 256) s.row_order[i] = i;
     }
   } else {
-    const int nKB = zb_key_block_count(s.Skv);
+    const int nKB = stats_key_block_count(s.Skv);
     const int n = nKB * s.B * s.Hkv;
     if (s.keys_sorted) {
       const KeyCost cost{win, s.B * s.Hkv, s.Hkv, s.Sq, s.causal,
@@ -399,7 +404,9 @@ __global__ __launch_bounds__(256) void coalibi_key_norm_kernel(const T* __restri
   }
 }
 
-template <typename T, int D, bool CAUSAL>
+// SKIP: the tail skip (args.knorm holds the key norms); without it every key is processed and
+// the kernel carries none of the skip's per-tile test.
+template <typename T, int D, bool CAUSAL, bool SKIP>
 __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coalibi_fwd_kernel(FwdArgs args) {
   using C = FwdCfg<T, D>;
   using M = Mfma<T>;
@@ -453,7 +460,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   VTile vt_regs;
   kt_regs.load(Kp, (nkt - 1) * kFwdBN, Skv, tid);
   vt_regs.load(Vp, (nkt - 1) * kFwdBN, Skv, tid);
-  const bool tail_skip = args.knorm != nullptr && lam2 > 0.f;
+  const bool tail_skip = SKIP && lam2 > 0.f;
   float km = 0.f;
   if (tail_skip) {
     const float* kn = args.knorm + ((size_t)b * args.Hkv + hkv) * args.nKC;
@@ -496,10 +503,11 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   f32x16 acc[C::DT];
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
+  // zsum: the sigmoid sum of the keys processed so far (right of the current tile), in fp64;
+  // zr, its fp32 value, is the running offset of the tile's z.
   float m2 = kNegInf, lsum = 0.f, zr = 0.f;
-  // Inference callers pass no zb / lse: the statistics only the backward reads are skipped.
-  const bool write_zb = args.zb != nullptr;
-  float* __restrict__ zb_row = write_zb ? args.zb + (size_t)bh * args.nZB * Sq + row : nullptr;
+  double zsum = 0.0;
+  if (args.flags != nullptr && blockIdx.x == 0 && tid < kStatsHeader) args.flags[tid] = tid == 0 ? args.order_flags : 0;
 
   int kt_end = 0;  // the loop's lower bound, raised by the tail skip
   for (int kt = nkt - 1; kt >= kt_end; --kt) {
@@ -537,17 +545,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
       continue;
     }
     const bool masked = (CAUSAL && k0 + kFwdBN - 1 > wrow0) || (k0 + kFwdBN > Skv);
-    float zst0, zst1;
+    float btot[2];
     if (masked)
-      fwd_tile<T, D, CAUSAL, true>(sK, sV, qf, acc, m2, lsum, zr, zst0, zst1, k0, row, lane, Skv, tile_sc2,
-                                   lam2);
+      fwd_tile<T, D, CAUSAL, true>(sK, sV, qf, acc, m2, lsum, zr, btot, k0, row, lane, Skv, tile_sc2, lam2);
     else
-      fwd_tile<T, D, CAUSAL, false>(sK, sV, qf, acc, m2, lsum, zr, zst0, zst1, k0, row, lane, Skv, tile_sc2,
-                                    lam2);
-    if (write_zb && hh == 0 && row_ok) {
-      zb_row[(size_t)(2 * kt) * Sq] = zst0;
-      if (k0 + 32 < Skv) zb_row[(size_t)(2 * kt + 1) * Sq] = zst1;
-    }
+      fwd_tile<T, D, CAUSAL, false>(sK, sV, qf, acc, m2, lsum, zr, btot, k0, row, lane, Skv, tile_sc2, lam2);
+    zsum += (double)btot[1];  // right block first, as the keys are walked
+    zsum += (double)btot[0];
+    zr = (float)zsum;
     if (!kPrefetchKV && kt > 0) {
       kt_regs.load(Kp, (kt - 1) * kFwdBN, Skv, tid);
       vt_regs.load(Vp, (kt - 1) * kFwdBN, Skv, tid);
@@ -582,6 +587,11 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
     }
     if (hh == 0 && args.lse != nullptr)
       args.lse[(size_t)bh * Sq + row] = ltot > 0.f ? (m2 + log2f(ltot)) * kLn2 : kNegInf;
+    if (hh == 0 && args.rsum != nullptr) {  // R as hi + lo, exact to about 2^-48 of it
+      const float hi = (float)zsum;
+      args.rsum[(size_t)bh * Sq + row] = hi;
+      args.rsum[(size_t)args.B * args.Hq * Sq + (size_t)bh * Sq + row] = (float)(zsum - (double)hi);
+    }
   }
 }
 
@@ -592,10 +602,11 @@ hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
   static_assert(kFwdBM == kSkipRows, "kstart entries are per forward row block");
   FwdArgs f = a;
   const bool rows_sorted = row_order_fits(a.B, a.Hq, a.Sq);
+  f.order_flags = 0;
   if (a.knorm != nullptr) {
+    const bool keys_sorted = key_order_used(a.B, a.Hq, a.Hkv, a.Skv);
     const ScheduleArgs sched{a.slopes, a.row_order, a.key_order, a.B, a.Hq, a.Hkv, a.Sq, a.Skv, CAUSAL ? 1 : 0,
-                             rows_sorted ? 1 : 0, key_order_used(a.B, a.Hq, a.Hkv, a.Skv) ? 1 : 0,
-                             order_window<T>()};
+                             rows_sorted ? 1 : 0, keys_sorted ? 1 : 0, order_window<T>()};
     // The key table needs the row table's work-group before it (work-group 1 writes it).
     const int nSched = a.row_order == nullptr ? 0 : (a.key_order != nullptr ? 2 : 1);
     hipLaunchKernelGGL((coalibi_key_norm_kernel<T, D>), dim3(nSched + a.nKC * a.B * a.Hq), dim3(256), 0, stream,
@@ -603,11 +614,18 @@ hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
                        sched);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // The backward follows a table only where it was sorted; an unsorted one holds the index
+    // order, which the fixed orders of the kernels beat (their heads rotate over the XCDs).
+    if (a.row_order != nullptr && rows_sorted) f.order_flags |= kFlagRowOrder;
+    if (a.key_order != nullptr && keys_sorted) f.order_flags |= kFlagKeyOrder;
   }
   if (a.knorm == nullptr || !rows_sorted) f.row_order = nullptr;  // no sorted table: the fixed order
   const int nQB = (a.Sq + kFwdBM - 1) / kFwdBM;
   const int grid = nQB * a.B * a.Hq;
-  hipLaunchKernelGGL((coalibi_fwd_kernel<T, D, CAUSAL>), dim3(grid), dim3(256), 0, stream, f);
+  if (a.knorm != nullptr)
+    hipLaunchKernelGGL((coalibi_fwd_kernel<T, D, CAUSAL, true>), dim3(grid), dim3(256), 0, stream, f);
+  else
+    hipLaunchKernelGGL((coalibi_fwd_kernel<T, D, CAUSAL, false>), dim3(grid), dim3(256), 0, stream, f);
   return hipGetLastError();
 }
 

@@ -9,19 +9,25 @@ constexpr float kLog2eHost = 1.4426950408889634f;
 
 // Tensors are contiguous row-major: q/o/dout/dq (B, Hq, Sq, D),
 // k/v/dk/dv (B, Hkv, Skv, D).  Query head h reads key/value head h / (Hq/Hkv).
-// zb (penalty statistics written by the forward, read by the backward) is
-// (B*Hq, nZB, Sq) fp32 with nZB = ceil(Skv/32): zb[bh][J][i] = sum of
-// sigmoid(p_ik) over valid keys k >= 32*J of row i.  The same buffer continues with
-// two small arrays:
-//   kstart (B*Hq, nQB) int32, nQB = ceil(Sq/128): the first key the forward processed
-//     for each 128-row block.  Every key left of it has a softmax weight below
-//     2^-skip_log2 of its row's total in every row of the block (the tail skip below);
-//     the backward passes skip the same keys, and zb of those blocks is not written;
+//
+// Statistics the forward saves for the backward besides LSE ("stats", int32 / fp32 words,
+// O(B*Hq*S) in all):
+//   header (kStatsHeader words): word 0 holds flags -- bit 0: row_order is a work order the
+//     key-norm launch wrote, bit 1: key_order likewise; without a bit the kernels that would
+//     read the table use their fixed order instead; the other header words are zero;
+//   kstart (B*Hq, nQB) int32, nQB = ceil(Sq/128): the first key the forward processed for
+//     each 128-row block (0 when the tail skip is off).  Every key left of it has a softmax
+//     weight below 2^-skip_log2 of its row's total in every row of the block (the tail skip
+//     below); the backward passes skip the same keys;
 //   knorm (B*Hq, nKC) fp32, nKC = ceil(Skv/kNormKeys): max_k |k|_2 over each chunk of
 //     kNormKeys keys of key head b*Hkv + h in its first B*Hkv rows, zero in the rest;
 //   row_order (B*Hq*nQB) int32: the work order of the forward and pass 1 (below);
 //   key_order (B*Hq*nKB) int32, nKB = ceil(Skv/64): the work order of pass 2 over its
-//     B*Hkv*nKB key blocks (written, and read, only when Hq == Hkv).
+//     B*Hkv*nKB key blocks (written, and read, only when Hq == Hkv);
+//   rsum (2, B*Hq, Sq) fp32: R_i, the sum of sigmoid(p_ik) over the keys the forward processed
+//     (k >= kstart), summed with compensation and saved as hi + lo.  It takes the place of the
+//     reference's RowSigTotal (co_alibi_attn.py:37): backward pass 1 walks the keys left to
+//     right and rebuilds z at each block start as R minus the sigma it has passed.
 //
 // Tail skip.  In the log2 domain a row's logit for key k is a_k = t_k - lam2 * z_k with
 // t_k = q.k * sm_scale * log2(e) and z_k = sum of sigmoids of the visible keys >= k.  The
@@ -40,16 +46,25 @@ constexpr float kLog2eHost = 1.4426950408889634f;
 //   fp32: 64 -- the validation mode stays within S * 2^-64 of the unskipped result.
 // The backward leaves out the same keys; their dA = s (dS - D) terms are below the same
 // fraction of the row's scale.
+// The skip is a library setting (co_alibi_set_tail_skip, on by default): with it off the
+// forward launches no key-norm kernel, processes every key and records kstart = 0.
+constexpr int kStatsHeader = 4;
+constexpr int kFlagRowOrder = 1;
+constexpr int kFlagKeyOrder = 2;
 constexpr int kNormKeys = 256;
 template <typename T>
 constexpr float skip_log2() {
   return sizeof(T) == 4 ? 64.0f : (__is_same(T, __bf16) ? 32.0f : 26.0f);
 }
 constexpr int kSkipRows = 128;  // rows per kstart entry: the forward's and pass 1's row block
-inline int zb_kstart_count(int Sq) { return (Sq + kSkipRows - 1) / kSkipRows; }
-inline int zb_knorm_count(int Skv) { return (Skv + kNormKeys - 1) / kNormKeys; }
+// kstart as the backward kernels read it.  It is device data the host cannot check without a
+// synchronisation: a value outside [0, Skv] (not written by the forward) counts as 0, so no
+// value moves a tile or a record address past the key range.
+__device__ __forceinline__ int valid_kstart(int ks, int Skv) { return ks >= 0 && ks <= Skv ? ks : 0; }
+inline int stats_kstart_count(int Sq) { return (Sq + kSkipRows - 1) / kSkipRows; }
+inline int stats_knorm_count(int Skv) { return (Skv + kNormKeys - 1) / kNormKeys; }
 constexpr int kOrderKeyBlock = 64;  // keys per pass-2 work-group (16-bit kernels)
-__host__ __device__ inline int zb_key_block_count(int Skv) { return (Skv + kOrderKeyBlock - 1) / kOrderKeyBlock; }
+__host__ __device__ inline int stats_key_block_count(int Skv) { return (Skv + kOrderKeyBlock - 1) / kOrderKeyBlock; }
 
 // Work orders.  The tail skip makes a work-group's cost depend on its head's slope: a
 // 128-row block of a steep head processes a few key tiles, one of a flat head up to all of
@@ -69,10 +84,10 @@ __host__ __device__ inline int zb_key_block_count(int Skv) { return (Skv + kOrde
 // grids keep the fixed orders.
 constexpr long long kOrderMaxItems = 1 << 20;
 inline bool row_order_fits(int B, int Hq, int Sq) {
-  return static_cast<long long>(B) * Hq * zb_kstart_count(Sq) <= kOrderMaxItems;
+  return static_cast<long long>(B) * Hq * stats_kstart_count(Sq) <= kOrderMaxItems;
 }
 inline bool key_order_fits(int B, int Hkv, int Skv) {
-  return static_cast<long long>(B) * Hkv * zb_key_block_count(Skv) <= kOrderMaxItems;
+  return static_cast<long long>(B) * Hkv * stats_key_block_count(Skv) <= kOrderMaxItems;
 }
 // Pass 2 follows key_order with one query head per key head only: with grouped heads the
 // sorted order measured slower than balanced_item (coalibi_common.h), which keeps runs of key
@@ -88,11 +103,13 @@ struct FwdArgs {
   const void* v;
   const float* slopes;  // (Hq,) penalty slope per query head
   void* o;
-  float* lse;  // (B*Hq, Sq) natural-log log-sum-exp
-  float* zb;
+  float* lse;          // (B*Hq, Sq) natural-log log-sum-exp, or NULL
   int* kstart;         // (B*Hq, nQB), written when not NULL (the backward's statistics)
   const float* knorm;  // (B*Hq, nKC) chunk maxima of |k|, filled before the forward; NULL: no tail skip
-  int B, Hq, Hkv, Sq, Skv, nZB, nKC;
+  int* flags;          // the statistics' header, written by work-group 0 when not NULL
+  int order_flags;     // its flags word: which work orders the key-norm launch wrote
+  float* rsum;         // (2, B*Hq, Sq) row sigmoid totals (hi, lo), written when not NULL
+  int B, Hq, Hkv, Sq, Skv, nKC;
   float sc2;  // sm_scale * log2(e)
   // Work orders (above): written by the key-norm launch when not NULL (key_order only with
   // row_order); the forward follows row_order when it is sorted (row_order_fits).
@@ -127,8 +144,11 @@ inline size_t score_records_per_head(int Sq, int Skv, bool causal) {
   return score_record(J, J, nQ32, true);  // records of the blocks before J
 }
 
-// Backward scratch: dsum (B*Hq, Sq) holds dO_i . O_i, cb (B*Hq, nZB, Sq)
-// holds sum over keys k < 32*J of dA_ik for every 32-key block J (recompute path only).
+// Backward scratch: dsum (B*Hq, Sq) holds dO_i . O_i.  The recompute path (pass 2 recomputes s
+// and dS) adds zb and cb, (B*Hq, nZB, Sq) fp32 each with nZB = ceil(Skv/32): for every 32-key
+// block J, zb[J][i] = sum of sigmoid(p_ik) over the keys k >= 32J of row i and cb[J][i] = sum of
+// dA_ik over the keys k < 32J, written by pass 1 for the blocks it processes.  The score-store
+// path needs neither.
 struct BwdArgs {
   const void* dout;
   const void* q;
@@ -136,18 +156,20 @@ struct BwdArgs {
   const void* v;
   const void* o;
   const float* lse;
-  const float* zb;
+  const float* rsum;  // (2, B*Hq, Sq): the forward's row sigmoid totals, hi and lo parts
   const float* slopes;
   void* dq;
   void* dk;
   void* dv;
   float* dsum;
+  float* zb;
   float* cb;
   const int* kstart;  // (B*Hq, nQB): keys left of kstart are skipped (see above)
-  void* scores;       // score store (above), or NULL: pass 2 recomputes s and dS from cb
+  const int* flags;   // the forward's flags word: which of the work orders below it wrote
+  void* scores;       // score store (above), or NULL: pass 2 recomputes s and dS from zb / cb
   size_t score_head;  // records per (b, h)
-  const int* row_order;  // pass 1's work order (above), or NULL: the fixed order
-  const int* key_order;  // pass 2's work order for 64-key work-groups, or NULL
+  const int* row_order;  // pass 1's work order (above) when flagged, or NULL: the fixed order
+  const int* key_order;  // pass 2's work order for 64-key work-groups when flagged, or NULL
   int B, Hq, Hkv, Sq, Skv, nZB;
   float sc2;
   float sm_scale;
@@ -182,14 +204,15 @@ struct DecodeArgs {
 // Split-K work-groups the decode aims at per CU: one round of the two that are resident.
 constexpr int kDecodeWGsPerCU = 2;
 
-// Forward; with a.knorm it first launches the key-norm kernel that fills it.
+// Forward; with a.knorm (the tail skip) it first launches the key-norm kernel that fills it.
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 
 template <typename T, int D>
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
 
-// stages: bit 0 = pass 1 (dq, dsum, and cb or the score store), bit 1 = pass 2 (dk, dv; needs pass 1's output).
+// stages: bit 0 = pass 1 (dq, dsum, and zb / cb or the score store), bit 1 = pass 2 (dk, dv; needs pass
+// 1's output).
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream);
 

@@ -1,8 +1,8 @@
 // PyTorch-ROCm operators over the C ABI of libco_alibi (include/co_alibi.h).
 //
-//   co_alibi::fwd(q, k, v, slopes, causal, sm_scale, with_stats) -> (o, lse, zb)
-//   co_alibi::bwd(do, q, k, v, o, lse, zb, slopes, causal, sm_scale) -> (dq, dk, dv)
-//   co_alibi::bwd_dq(do, q, k, v, o, lse, zb, slopes, causal, sm_scale) -> dq
+//   co_alibi::fwd(q, k, v, slopes, causal, sm_scale, with_stats) -> (o, lse, stats)
+//   co_alibi::bwd(do, q, k, v, o, lse, stats, slopes, causal, sm_scale) -> (dq, dk, dv)
+//   co_alibi::bwd_dq(do, q, k, v, o, lse, stats, slopes, causal, sm_scale) -> dq
 //   co_alibi::decode(q, k_cache, v_cache, slopes, seq_lens, max_seq_len, sm_scale, with_lse) -> (o, lse)
 //
 // They replace the reference's two Triton launches with their buffer set-up
@@ -12,11 +12,14 @@
 // graph.  co_alibi::fwd carries its backward as a C++ autograd kernel: dQ alone runs backward
 // pass 1 only (co_alibi::bwd_dq); any key / value gradient runs both passes (co_alibi::bwd).
 // co_alibi::bwd uses the score store (pass 1 keeps s and dS, pass 2 reduces them) where the
-// library has it and its workspace is at most CO_ALIBI_SCORE_STORE_LIMIT_MB megabytes (an
-// environment variable read once; 16384 by default, 0 turns the store off).
+// library has it and its workspace fits: at most CO_ALIBI_SCORE_STORE_LIMIT_MB megabytes (an
+// environment variable read once; 16384 by default, 0 turns the store off) and at most half
+// of the device memory that is free or cached by torch's allocator at the call.  If allocating
+// it fails anyway, the backward takes the recompute path, whose workspace is O(S^2 / 32).
 // The shape functions for FakeTensor / meta tracing are registered from Python.
 #include <ATen/ATen.h>
 #include <ATen/core/dispatch/Dispatcher.h>
+#include <c10/hip/HIPCachingAllocator.h>
 #include <c10/hip/HIPGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/autograd.h>
@@ -60,9 +63,9 @@ Tensor slopes_f32(const Tensor& slopes, const Tensor& like) {
 
 Tensor empty_stats(const Tensor& q) { return at::empty({0}, q.options().dtype(at::kFloat)); }
 
-int64_t zb_numel(int64_t batch, int64_t heads_q, int64_t seq_q, int64_t seq_kv) {
-  return static_cast<int64_t>(co_alibi_zb_numel(static_cast<int>(batch), static_cast<int>(heads_q),
-                                                static_cast<int>(seq_q), static_cast<int>(seq_kv)));
+int64_t stats_numel(int64_t batch, int64_t heads_q, int64_t seq_q, int64_t seq_kv) {
+  return static_cast<int64_t>(co_alibi_stats_numel(static_cast<int>(batch), static_cast<int>(heads_q),
+                                                   static_cast<int>(seq_q), static_cast<int>(seq_kv)));
 }
 
 hipStream_t current_stream(const Tensor& t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
@@ -80,19 +83,19 @@ std::tuple<Tensor, Tensor, Tensor> fwd_hip(const Tensor& q_in, const Tensor& k_i
     if (!with_stats) return {o, empty_stats(q_in), empty_stats(q_in)};
     Tensor lse = at::full({batch, heads_q, seq_q}, -std::numeric_limits<float>::infinity(),
                           q_in.options().dtype(at::kFloat));
-    return {o, lse, at::empty({zb_numel(batch, heads_q, seq_q, seq_kv)}, q_in.options().dtype(at::kFloat))};
+    return {o, lse, at::zeros({stats_numel(batch, heads_q, seq_q, seq_kv)}, q_in.options().dtype(at::kFloat))};
   }
   c10::hip::HIPGuard guard(q_in.device().index());
   const Tensor q = aligned(q_in), k = aligned(k_in), v = aligned(v_in);
   const Tensor sl = slopes_f32(slopes, q);
   Tensor o = at::empty_like(q);
   Tensor lse = with_stats ? at::empty({batch, heads_q, seq_q}, q.options().dtype(at::kFloat)) : empty_stats(q);
-  Tensor zb = with_stats ? at::empty({zb_numel(batch, heads_q, seq_q, seq_kv)}, q.options().dtype(at::kFloat))
-                         : empty_stats(q);
+  Tensor stats = with_stats ? at::empty({stats_numel(batch, heads_q, seq_q, seq_kv)}, q.options().dtype(at::kFloat))
+                            : empty_stats(q);
   const int code = dtype_code(q.scalar_type());
   if (with_stats) {
     check(co_alibi_fwd(code, q.data_ptr(), k.data_ptr(), v.data_ptr(), sl.data_ptr<float>(), o.data_ptr(),
-                       lse.data_ptr<float>(), zb.data_ptr<float>(), batch, heads_q, heads_kv, seq_q, seq_kv, head_dim,
+                       lse.data_ptr<float>(), stats.data_ptr<float>(), batch, heads_q, heads_kv, seq_q, seq_kv, head_dim,
                        causal ? 1 : 0, static_cast<float>(sm_scale), current_stream(q)));
   } else {  // inference: the tail skip with only its key-norm and work-order scratch
     const size_t ws_bytes = co_alibi_fwd_inference_workspace_bytes(batch, heads_q, seq_q, seq_kv);
@@ -101,12 +104,12 @@ std::tuple<Tensor, Tensor, Tensor> fwd_hip(const Tensor& q_in, const Tensor& k_i
                                  ws.data_ptr(), ws_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim,
                                  causal ? 1 : 0, static_cast<float>(sm_scale), current_stream(q)));
   }
-  return {o, lse, zb};
+  return {o, lse, stats};
 }
 
 // --------------------------------------------------------------------------- backward
 
-// Largest workspace co_alibi::bwd takes for the score store.
+// Largest workspace co_alibi::bwd takes for the score store (the environment's limit).
 size_t score_store_limit() {
   static const size_t limit = [] {
     const char* e = std::getenv("CO_ALIBI_SCORE_STORE_LIMIT_MB");
@@ -116,10 +119,21 @@ size_t score_store_limit() {
   return limit;
 }
 
+// Device memory a new allocation can take on the current device: what the driver reports free
+// plus what torch's caching allocator holds unused.
+size_t device_memory_available() {
+  size_t free_b = 0, total_b = 0;
+  if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return 0;
+  const auto stats = c10::hip::HIPCachingAllocator::getDeviceStats(c10::hip::current_device());
+  const size_t agg = static_cast<size_t>(c10::CachingAllocator::StatType::AGGREGATE);
+  const int64_t cached = stats.reserved_bytes[agg].current - stats.allocated_bytes[agg].current;
+  return free_b + static_cast<size_t>(cached > 0 ? cached : 0);
+}
+
 // Shared set-up of both backward operators; stages 1 = pass 1 only (dq), 3 = both passes.
 std::tuple<Tensor, Tensor, Tensor> bwd_common(int stages, const Tensor& do_in, const Tensor& q_in, const Tensor& k_in,
                                               const Tensor& v_in, const Tensor& o_in, const Tensor& lse_in,
-                                              const Tensor& zb_in, const Tensor& slopes, bool causal,
+                                              const Tensor& stats_in, const Tensor& slopes, bool causal,
                                               double sm_scale) {
   const int64_t batch = q_in.size(0), heads_q = q_in.size(1), seq_q = q_in.size(2), head_dim = q_in.size(3);
   const int64_t heads_kv = k_in.size(1), seq_kv = k_in.size(2);
@@ -130,28 +144,35 @@ std::tuple<Tensor, Tensor, Tensor> bwd_common(int stages, const Tensor& do_in, c
   c10::hip::HIPGuard guard(q_in.device().index());
   const Tensor q = aligned(q_in), k = aligned(k_in), v = aligned(v_in), o = aligned(o_in);
   const Tensor dout = aligned(do_in.to(q.scalar_type()));
-  const Tensor lse = lse_in.contiguous(), zb = zb_in.contiguous();
+  const Tensor lse = lse_in.contiguous(), stats = stats_in.contiguous();
   const Tensor sl = slopes_f32(slopes, q);
   Tensor dq = at::empty_like(q);
   Tensor dk = stages & 2 ? at::empty_like(k) : Tensor();
   Tensor dv = stages & 2 ? at::empty_like(v) : Tensor();
   const int code = dtype_code(q.scalar_type());
   size_t ws_bytes = co_alibi_bwd_workspace_bytes(batch, heads_q, seq_q, seq_kv);
+  Tensor ws;
   if (stages & 2) {
     const size_t store_bytes =
         co_alibi_bwd_score_store_workspace_bytes(code, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal ? 1 : 0);
-    if (store_bytes != 0 && store_bytes <= score_store_limit()) ws_bytes = store_bytes;
+    if (store_bytes != 0 && store_bytes <= score_store_limit() && store_bytes <= device_memory_available() / 2) {
+      try {
+        ws = at::empty({static_cast<int64_t>(store_bytes)}, q.options().dtype(at::kByte));
+        ws_bytes = store_bytes;
+      } catch (const c10::OutOfMemoryError&) {  // the recompute path's smaller workspace below
+      }
+    }
   }
-  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  if (!ws.defined()) ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
   const hipStream_t st = current_stream(q);
   if (stages & 2) {
     check(co_alibi_bwd(code, dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                       lse.data_ptr<float>(), zb.data_ptr<float>(), sl.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(),
-                       dv.data_ptr(), ws.data_ptr(), ws_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim,
-                       causal ? 1 : 0, static_cast<float>(sm_scale), st));
+                       lse.data_ptr<float>(), stats.data_ptr<float>(), sl.data_ptr<float>(), dq.data_ptr(),
+                       dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, batch, heads_q, heads_kv, seq_q,
+                       seq_kv, head_dim, causal ? 1 : 0, static_cast<float>(sm_scale), st));
   } else {
     check(co_alibi_bwd_dq(code, dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                          lse.data_ptr<float>(), zb.data_ptr<float>(), sl.data_ptr<float>(), dq.data_ptr(),
+                          lse.data_ptr<float>(), stats.data_ptr<float>(), sl.data_ptr<float>(), dq.data_ptr(),
                           ws.data_ptr(), ws_bytes, batch, heads_q, heads_kv, seq_q, seq_kv, head_dim, causal ? 1 : 0,
                           static_cast<float>(sm_scale), st));
   }
@@ -159,14 +180,14 @@ std::tuple<Tensor, Tensor, Tensor> bwd_common(int stages, const Tensor& do_in, c
 }
 
 std::tuple<Tensor, Tensor, Tensor> bwd_hip(const Tensor& dout, const Tensor& q, const Tensor& k, const Tensor& v,
-                                           const Tensor& o, const Tensor& lse, const Tensor& zb, const Tensor& slopes,
-                                           bool causal, double sm_scale) {
-  return bwd_common(3, dout, q, k, v, o, lse, zb, slopes, causal, sm_scale);
+                                           const Tensor& o, const Tensor& lse, const Tensor& stats,
+                                           const Tensor& slopes, bool causal, double sm_scale) {
+  return bwd_common(3, dout, q, k, v, o, lse, stats, slopes, causal, sm_scale);
 }
 
 Tensor bwd_dq_hip(const Tensor& dout, const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& o,
-                  const Tensor& lse, const Tensor& zb, const Tensor& slopes, bool causal, double sm_scale) {
-  return std::get<0>(bwd_common(1, dout, q, k, v, o, lse, zb, slopes, causal, sm_scale));
+                  const Tensor& lse, const Tensor& stats, const Tensor& slopes, bool causal, double sm_scale) {
+  return std::get<0>(bwd_common(1, dout, q, k, v, o, lse, stats, slopes, causal, sm_scale));
 }
 
 // ----------------------------------------------------------------------------- decode
@@ -215,27 +236,27 @@ std::tuple<Tensor, Tensor, Tensor> call_fwd(const Tensor& q, const Tensor& k, co
 }
 
 // Autograd function of co_alibi::fwd (the role of the reference's CoALIBIAttention,
-// co_alibi_attn.py:24-135): saves q, k, v, o, lse, zb and the slopes; lse and zb carry no
+// co_alibi_attn.py:24-135): saves q, k, v, o, lse, stats and the slopes; lse and stats carry no
 // gradient; slopes, causal, sm_scale and with_stats get none.
 class FwdFunction : public torch::autograd::Function<FwdFunction> {
  public:
   static torch::autograd::variable_list forward(torch::autograd::AutogradContext* ctx, const Tensor& q,
                                                 const Tensor& k, const Tensor& v, const Tensor& slopes, bool causal,
                                                 double sm_scale, bool with_stats) {
-    Tensor o, lse, zb;
+    Tensor o, lse, stats;
     {
       at::AutoDispatchBelowADInplaceOrView below;
-      std::tie(o, lse, zb) = call_fwd(q, k, v, slopes, causal, sm_scale, with_stats);
+      std::tie(o, lse, stats) = call_fwd(q, k, v, slopes, causal, sm_scale, with_stats);
     }
-    ctx->save_for_backward({q, k, v, o, lse, zb, slopes});
+    ctx->save_for_backward({q, k, v, o, lse, stats, slopes});
     ctx->saved_data["causal"] = causal;
     ctx->saved_data["sm_scale"] = sm_scale;
     ctx->saved_data["with_stats"] = with_stats;
-    ctx->mark_non_differentiable({lse, zb});
-    // lse and zb never get a gradient: without this the engine would fill zero tensors for them
-    // before every backward (zb is O(S^2 / 32) floats).
+    ctx->mark_non_differentiable({lse, stats});
+    // lse and stats never get a gradient: without this the engine would fill zero tensors for
+    // them before every backward.
     ctx->set_materialize_grads(false);
-    return {o, lse, zb};
+    return {o, lse, stats};
   }
 
   static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
@@ -243,8 +264,8 @@ class FwdFunction : public torch::autograd::Function<FwdFunction> {
     TORCH_CHECK(ctx->saved_data["with_stats"].toBool(),
                 "co_alibi::fwd ran with with_stats=False (inference) and has no backward");
     const auto saved = ctx->get_saved_variables();
-    const Tensor &q = saved[0], &k = saved[1], &v = saved[2], &o = saved[3], &lse = saved[4], &zb = saved[5],
-                 &slopes = saved[6];
+    const Tensor &q = saved[0], &k = saved[1], &v = saved[2], &o = saved[3], &lse = saved[4],
+                 &stats = saved[5], &slopes = saved[6];
     const bool causal = ctx->saved_data["causal"].toBool();
     const double sm_scale = ctx->saved_data["sm_scale"].toDouble();
     const bool need_q = ctx->needs_input_grad(0), need_k = ctx->needs_input_grad(1), need_v = ctx->needs_input_grad(2);
@@ -254,11 +275,11 @@ class FwdFunction : public torch::autograd::Function<FwdFunction> {
       if (!need_k && !need_v) {
         static const auto op_dq =
             c10::Dispatcher::singleton().findSchemaOrThrow("co_alibi::bwd_dq", "").typed<decltype(bwd_dq_hip)>();
-        if (need_q) dq = op_dq.call(dout, q, k, v, o, lse, zb, slopes, causal, sm_scale);
+        if (need_q) dq = op_dq.call(dout, q, k, v, o, lse, stats, slopes, causal, sm_scale);
       } else {
         static const auto op =
             c10::Dispatcher::singleton().findSchemaOrThrow("co_alibi::bwd", "").typed<decltype(bwd_hip)>();
-        std::tie(dq, dk, dv) = op.call(dout, q, k, v, o, lse, zb, slopes, causal, sm_scale);
+        std::tie(dq, dk, dv) = op.call(dout, q, k, v, o, lse, stats, slopes, causal, sm_scale);
         if (!need_q) dq = Tensor();
         if (!need_k) dk = Tensor();
         if (!need_v) dv = Tensor();
@@ -279,9 +300,9 @@ std::tuple<Tensor, Tensor, Tensor> fwd_autograd(const Tensor& q, const Tensor& k
 TORCH_LIBRARY(co_alibi, m) {
   m.def("fwd(Tensor q, Tensor k, Tensor v, Tensor slopes, bool causal, float sm_scale, bool with_stats) -> "
         "(Tensor, Tensor, Tensor)");
-  m.def("bwd(Tensor do, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor zb, Tensor slopes, bool causal, "
-        "float sm_scale) -> (Tensor, Tensor, Tensor)");
-  m.def("bwd_dq(Tensor do, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor zb, Tensor slopes, "
+  m.def("bwd(Tensor do, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor stats, Tensor slopes, "
+        "bool causal, float sm_scale) -> (Tensor, Tensor, Tensor)");
+  m.def("bwd_dq(Tensor do, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor stats, Tensor slopes, "
         "bool causal, float sm_scale) -> Tensor");
   m.def("decode(Tensor q, Tensor k_cache, Tensor v_cache, Tensor slopes, Tensor? seq_lens, SymInt max_seq_len, "
         "float sm_scale, bool with_lse) -> (Tensor, Tensor)");

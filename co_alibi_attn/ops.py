@@ -29,7 +29,7 @@ from torch import Tensor
 
 from . import _native
 
-__all__ = ["fwd", "bwd", "bwd_dq", "backward_for", "decode", "zb_numel", "TORCH_LIB_PATH"]
+__all__ = ["fwd", "bwd", "bwd_dq", "backward_for", "decode", "stats_numel", "TORCH_LIB_PATH"]
 
 TORCH_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libco_alibi_torch.so")
 
@@ -73,28 +73,29 @@ else:
     fwd = bwd = bwd_dq = decode = _unavailable
 
 
-def zb_numel(batch: int, heads_q: int, seq_q: int, seq_kv: int) -> int:
-    """fp32 elements of the forward's penalty statistics (the value co_alibi_zb_numel of
-    the C ABI returns): B*Hq * (ceil(Skv/32) * Sq  zb blocks, + ceil(Sq/128)  first
-    processed key per 128-row block, + ceil(Skv/256)  key-norm chunk maxima, + ceil(Sq/128)
-    and ceil(Skv/64)  work orders of the row and key blocks)."""
-    return batch * heads_q * (((seq_kv + 31) // 32) * seq_q + 2 * ((seq_q + 127) // 128) + (seq_kv + 255) // 256
-                              + (seq_kv + 63) // 64)
+def stats_numel(batch: int, heads_q: int, seq_q: int, seq_kv: int) -> int:
+    """4-byte words of the forward's saved statistics besides LSE (the value co_alibi_stats_numel
+    of the C ABI returns), O(B*Hq*S): a 4-word header, then B*Hq * (ceil(Sq/128)  first processed
+    key per 128-row block, + ceil(Skv/256)  key-norm chunk maxima, + ceil(Sq/128) and
+    ceil(Skv/64)  work orders of the row and key blocks, + 2*Sq  each row's sigmoid sum as a
+    compensated hi / lo pair)."""
+    return 4 + batch * heads_q * (2 * ((seq_q + 127) // 128) + (seq_kv + 255) // 256 + (seq_kv + 63) // 64
+                                  + 2 * seq_q)
 
 
 def _empty_stats(q: Tensor) -> Tensor:
     return q.new_empty((0,), dtype=torch.float32)
 
 
-def backward_for(needs_input_grad, do, q, k, v, o, lse, zb, slopes, causal, sm_scale):
+def backward_for(needs_input_grad, do, q, k, v, o, lse, stats, slopes, causal, sm_scale):
     """(dq, dk, dv) for the inputs whose flag in ``needs_input_grad`` (q, k, v first) is set,
     None for the others -- the rule of co_alibi::fwd's C++ autograd kernel, for Python autograd
     functions over the same operators.  dK needs backward pass 1's per-row statistics, so pass 1
     runs whenever any gradient is wanted; pass 2 runs only when dK or dV is."""
     need_q, need_k, need_v = needs_input_grad[:3]
     if not (need_k or need_v):
-        return (bwd_dq(do, q, k, v, o, lse, zb, slopes, causal, sm_scale) if need_q else None), None, None
-    dq, dk, dv = bwd(do, q, k, v, o, lse, zb, slopes, causal, sm_scale)
+        return (bwd_dq(do, q, k, v, o, lse, stats, slopes, causal, sm_scale) if need_q else None), None, None
+    dq, dk, dv = bwd(do, q, k, v, o, lse, stats, slopes, causal, sm_scale)
     return dq if need_q else None, dk if need_k else None, dv if need_v else None
 
 
@@ -106,26 +107,26 @@ def _register_fakes() -> None:
 
     @torch.library.register_fake("co_alibi::fwd")
     def _fwd_fake(q, k, v, slopes, causal, sm_scale, with_stats):
-        """o (B, Hq, Sq, D) in q.dtype; with_stats: lse (B, Hq, Sq) and zb (zb_numel(...),) in
-        fp32, else both empty.  Causal zb entries of 32-key blocks wholly past a row's diagonal
-        are left unwritten by the kernel; no reader needs them."""
+        """o (B, Hq, Sq, D) in q.dtype; with_stats: lse (B, Hq, Sq) in fp32 and the statistics
+        (stats_numel(...),) as 4-byte words, else both empty.  With the tail skip off the key
+        norms and work orders in the statistics are left unwritten (their header says so)."""
         batch, heads_q, seq_q, _ = q.shape
         o = torch.empty_like(q, memory_format=torch.contiguous_format)
         if not with_stats:
             return o, _empty_stats(q), _empty_stats(q)
         lse = q.new_empty((batch, heads_q, seq_q), dtype=torch.float32)
-        zb = q.new_empty((zb_numel(batch, heads_q, seq_q, k.shape[2]),), dtype=torch.float32)
-        return o, lse, zb
+        stats = q.new_empty((stats_numel(batch, heads_q, seq_q, k.shape[2]),), dtype=torch.float32)
+        return o, lse, stats
 
     @torch.library.register_fake("co_alibi::bwd")
-    def _bwd_fake(do, q, k, v, o, lse, zb, slopes, causal, sm_scale):
+    def _bwd_fake(do, q, k, v, o, lse, stats, slopes, causal, sm_scale):
         """(dq, dk, dv) in the input dtype; dk / dv have k's head count (summed over each group)."""
         cf = torch.contiguous_format
         return (torch.empty_like(q, memory_format=cf), torch.empty_like(k, memory_format=cf),
                 torch.empty_like(v, memory_format=cf))
 
     @torch.library.register_fake("co_alibi::bwd_dq")
-    def _bwd_dq_fake(do, q, k, v, o, lse, zb, slopes, causal, sm_scale):
+    def _bwd_dq_fake(do, q, k, v, o, lse, stats, slopes, causal, sm_scale):
         """dq alone (backward pass 1), bit-identical to co_alibi::bwd's dq."""
         return torch.empty_like(q, memory_format=torch.contiguous_format)
 

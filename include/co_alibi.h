@@ -45,19 +45,31 @@ enum co_alibi_status {
   CO_ALIBI_ELAUNCH = 3       /* the HIP runtime refused the launch */
 };
 
-/* Number of fp32 elements of the penalty statistics `zb` that co_alibi_fwd
- * writes and co_alibi_bwd reads: B*Hq * (ceil(Skv/32) * Sq + 2 * ceil(Sq/128) +
- * ceil(Skv/256) + ceil(Skv/64)).  The first B*Hq*ceil(Skv/32)*Sq are zb[bh][J][i], the
- * sum of sigmoid(sm_scale * q_i.k_j) over the visible keys j >= 32*J of row i; they take
- * the place of the reference's RowSigTotal (co_alibi_attn.py:37).  Then, per
- * 128-row block, the first key the forward processed (keys further left carry
- * softmax weights below 2^-T of their row's total, T = 26 in fp16, 32 in bf16 and
- * 64 in fp32, and are skipped by forward and backward alike; zb is not written for
- * them); per 256-key chunk of each key head, the largest |k|; and the order in which
- * the kernels take their row and key blocks (int32), which the forward writes. */
-size_t co_alibi_zb_numel(int batch, int heads_q, int seq_q, int seq_kv);
+/* Number of 4-byte words of the statistics `stats` that co_alibi_fwd writes beside lse and
+ * co_alibi_bwd reads: 4 + B*Hq * (2 * ceil(Sq/128) + ceil(Skv/256) + ceil(Skv/64) + 2 * Sq),
+ * O(B*Hq*S).  A 4-word header (flags: which work orders the forward wrote); per 128-row block
+ * the first key the forward processed (int32; keys further left carry softmax weights below
+ * 2^-T of their row's total, T = 26 in fp16, 32 in bf16 and 64 in fp32, and are skipped by
+ * forward and backward alike; 0 when the tail skip is off); per 256-key chunk of each key head
+ * the largest |k|; the order in which the kernels take their row and key blocks (int32); and
+ * per row the sum of the sigmoids of the processed keys, as an fp32 hi part (B*Hq*Sq) and its
+ * compensation (B*Hq*Sq).  That row sum is the reference's RowSigTotal (co_alibi_attn.py:37);
+ * the backward rebuilds the penalty from it. */
+size_t co_alibi_stats_numel(int batch, int heads_q, int seq_q, int seq_kv);
 
-/* Bytes of device scratch co_alibi_bwd needs. */
+/* The tail skip as a library setting, for every later co_alibi_fwd and co_alibi_fwd_inference
+ * call of the process: enabled != 0 (the default) leaves out the keys whose softmax weight is
+ * provably below 2^-T of their row's total (above), 0 makes the forward process every key, as
+ * the reference does (co_alibi_fwd_kernel.py:66-71), with no key-norm launch and no per-tile
+ * test.  The backward follows what its forward recorded.  Returns the previous setting.  No
+ * counterpart in the reference, which processes every key. */
+int co_alibi_set_tail_skip(int enabled);
+int co_alibi_tail_skip(void);
+
+/* Bytes of device scratch co_alibi_bwd needs (the recompute path): per-row dO.O, then per 32-key
+ * block of every row the sigmoid sum from the block start on and the dA sum before it,
+ * 2 * B*Hq * ceil(Skv/32) * Sq fp32 -- transient, the backward's own, where the reference holds
+ * its per-query-block dK / dV partials (co_alibi_attn.py:83-99). */
 size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_kv);
 
 /* Bytes of device scratch that switch the backward to the score store: pass 1 keeps the
@@ -65,7 +77,8 @@ size_t co_alibi_bwd_workspace_bytes(int batch, int heads_q, int seq_q, int seq_k
  * pairs that can be visible (about 2 * Sq * Skv bytes per batch and query head when causal,
  * twice that otherwise), and pass 2 reduces them into dk and dv instead of recomputing
  * them.  0 when dtype / head_dim have no such path (fp16 and bf16 at head_dim 64 and 128
- * have it) or when (heads_q / heads_kv) * ceil(seq_q / 8192) exceeds 256.  A workspace of at least this size selects the path; a smaller one (at least
+ * have it) or when (heads_q / heads_kv) * ceil(seq_q / 8192) exceeds 256.  A workspace of at
+ * least this size selects the path; a smaller one (at least
  * co_alibi_bwd_workspace_bytes) the recompute path.  co_alibi_bwd_dq and co_alibi_bwd_dkdv
  * must then get the same workspace and size.  No counterpart in the reference, whose
  * backward keeps per-query-block dK / dV partials instead (co_alibi_attn.py:83-133). */
@@ -73,17 +86,18 @@ size_t co_alibi_bwd_score_store_workspace_bytes(int dtype, int batch, int heads_
                                                 int seq_kv, int head_dim, int causal);
 
 /* Forward: writes o (B,Hq,Sq,D, dtype), lse (B,Hq,Sq, fp32 natural log-sum-exp
- * m_i + log(l_i), co_alibi_fwd_kernel.py:120) and zb.  The reference adds 1e-9
+ * m_i + log(l_i), co_alibi_fwd_kernel.py:120) and stats.  The reference adds 1e-9
  * to l_i there and in the O normaliser (:115); l_i >= 1 here, so that term is
- * below fp32 resolution and is left out.  lse and zb may be NULL (inference: the
- * statistics only co_alibi_bwd reads are then not written); o is the same. */
+ * below fp32 resolution and is left out.  lse and stats may be NULL (inference: the
+ * statistics only co_alibi_bwd reads are then not written, and every key is
+ * processed); o is the same. */
 int co_alibi_fwd(int dtype, const void* q, const void* k, const void* v, const float* slopes,
-                 void* o, float* lse, float* zb, int batch, int heads_q, int heads_kv, int seq_q,
+                 void* o, float* lse, float* stats, int batch, int heads_q, int heads_kv, int seq_q,
                  int seq_kv, int head_dim, int causal, float sm_scale, void* stream);
 
-/* Forward for inference with the tail skip: o only (no lse or zb), skipping the keys
+/* Forward for inference with the tail skip: o only (no lse or stats), skipping the keys
  * whose softmax weight is below 2^-T of the row total as co_alibi_fwd does with its
- * statistics (co_alibi_fwd with lse = zb = NULL computes every key).  workspace holds
+ * statistics (co_alibi_fwd with lse = stats = NULL computes every key).  workspace holds
  * co_alibi_fwd_inference_workspace_bytes(...) bytes (256-byte aligned): the largest |k|
  * per 256-key chunk of every key head and the order of the row blocks.  No counterpart in
  * the reference, whose forward always saves its statistics (co_alibi_attn.py:35-57). */
@@ -93,29 +107,29 @@ int co_alibi_fwd_inference(int dtype, const void* q, const void* k, const void* 
                            int heads_kv, int seq_q, int seq_kv, int head_dim, int causal, float sm_scale,
                            void* stream);
 
-/* Backward: given dout and the forward's q, k, v, o, lse, zb, writes dq
+/* Backward: given dout and the forward's q, k, v, o, lse, stats, writes dq
  * (B,Hq,Sq,D), dk and dv (B,Hkv,Skv,D), all in dtype.  For Hkv < Hq the key /
  * value gradients are summed over the query heads of each group.  workspace
  * must hold co_alibi_bwd_workspace_bytes(...) bytes (256-byte aligned). */
 int co_alibi_bwd(int dtype, const void* dout, const void* q, const void* k, const void* v,
-                 const void* o, const float* lse, const float* zb, const float* slopes, void* dq,
+                 const void* o, const float* lse, const float* stats, const float* slopes, void* dq,
                  void* dk, void* dv, void* workspace, size_t workspace_bytes, int batch, int heads_q,
                  int heads_kv, int seq_q, int seq_kv, int head_dim, int causal, float sm_scale,
                  void* stream);
 
 /* The two passes of co_alibi_bwd as separate calls, for callers that time or
  * schedule them apart.  co_alibi_bwd_dq writes dq and fills the workspace
- * (per-row dO.O and the per-32-key-block prefix of dA, or the score store); co_alibi_bwd_dkdv
+ * (per-row dO.O and the per-32-key-block sums, or the score store); co_alibi_bwd_dkdv
  * then writes dk and dv from that workspace.  Issued in this order on one
  * stream they are exactly co_alibi_bwd.  The reference runs both in one
  * kernel (co_alibi_attn/co_alibi_bwd_kernel.py:17-146). */
 int co_alibi_bwd_dq(int dtype, const void* dout, const void* q, const void* k, const void* v,
-                    const void* o, const float* lse, const float* zb, const float* slopes, void* dq,
+                    const void* o, const float* lse, const float* stats, const float* slopes, void* dq,
                     void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv,
                     int seq_q, int seq_kv, int head_dim, int causal, float sm_scale, void* stream);
 
 int co_alibi_bwd_dkdv(int dtype, const void* dout, const void* q, const void* k, const void* v,
-                      const float* lse, const float* zb, const float* slopes, void* dk, void* dv,
+                      const float* lse, const float* stats, const float* slopes, void* dk, void* dv,
                       void* workspace, size_t workspace_bytes, int batch, int heads_q, int heads_kv,
                       int seq_q, int seq_kv, int head_dim, int causal, float sm_scale, void* stream);
 
@@ -166,8 +180,8 @@ int co_alibi_probe_mfma(void* ticks, void* sink, int blocks, int iters, void* st
 /* Message describing the last failed call on this thread ("" if none). */
 const char* co_alibi_last_error(void);
 
-/* ABI version of this header: 5 (seq_q in co_alibi_fwd_inference_workspace_bytes; the
- * work orders in zb). */
+/* ABI version of this header: 6 (O(S) statistics, the row sigmoid sums in place of the
+ * per-block penalty sums; the tail-skip setting). */
 int co_alibi_abi_version(void);
 
 #ifdef __cplusplus

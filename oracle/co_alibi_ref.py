@@ -80,15 +80,22 @@ def _rows_forward(qr, k, v, lam, causal, scale, row0):
     return o, lse, s, sig, mask
 
 
+def _rows_terms(qr, dor, k, v, lam, causal, scale, row0):
+    """Per-pair terms of the backward for a block of query rows: (s, sigma, dA, mask) with
+    dA = s (dS - sum_j dS s) (model.py:38-39, 23, 62-66)."""
+    _, _, s, sig, mask = _rows_forward(qr, k, v, lam, causal, scale, row0)
+    ds = dor @ v.transpose(0, 1)                                          # model.py:62
+    dsum = (ds * s).sum(dim=-1, keepdim=True)                             # model.py:64
+    da = (s * (ds - dsum)).masked_fill(mask, 0.0)                         # model.py:65-66
+    return s, sig, da, mask
+
+
 def _rows_backward(qr, dor, k, v, lam, causal, scale, row0):
     """Backward for a block of query rows (model.py:57-76 with slope as benchmark_bwd_pass.py:89-91).
 
     Returns (dq rows, dk contribution, dv contribution)."""
-    _, _, s, sig, mask = _rows_forward(qr, k, v, lam, causal, scale, row0)
+    s, sig, da, mask = _rows_terms(qr, dor, k, v, lam, causal, scale, row0)
     dv = s.transpose(0, 1) @ dor                                          # model.py:61
-    ds = dor @ v.transpose(0, 1)                                          # model.py:62
-    dsum = (ds * s).sum(dim=-1, keepdim=True)                             # model.py:64
-    da = (s * (ds - dsum)).masked_fill(mask, 0.0)                         # model.py:65-66
     sig_prime = sig * (1.0 - sig)                                         # model.py:68
     c = torch.cumsum(da, dim=-1)                                          # model.py:69
     dp = (da - lam * sig_prime * c).masked_fill(mask, 0.0)                # model.py:71-73 (+ slope)

@@ -122,7 +122,7 @@ void check_attention(const char* name, int dtype, int B, int Hq, int Hkv, int Sq
   const double scale = 1.0 / std::sqrt((double)D);
   const size_t nq = (size_t)B * Hq * Sq * D, nkv = (size_t)B * Hkv * Skv * D, nrow = (size_t)B * Hq * Sq;
   DevBuf q(nq, dtype), k(nkv, dtype), v(nkv, dtype), dout(nq, dtype), o(nq, dtype), dq(nq, dtype), dk(nkv, dtype),
-      dv(nkv, dtype), lse(nrow, CO_ALIBI_F32), zb(co_alibi_zb_numel(B, Hq, Sq, Skv), CO_ALIBI_F32),
+      dv(nkv, dtype), lse(nrow, CO_ALIBI_F32), stats(co_alibi_stats_numel(B, Hq, Sq, Skv), CO_ALIBI_F32),
       sl(Hq, CO_ALIBI_F32);
   const std::vector<double> hq = q.upload(randn(nq, 1, 0.5)), hk = k.upload(randn(nkv, 2, 0.5)),
                             hv = v.upload(randn(nkv, 3, 0.5)), hdo = dout.upload(randn(nq, 4, 1.0));
@@ -137,10 +137,10 @@ void check_attention(const char* name, int dtype, int B, int Hq, int Hkv, int Sq
   void* ws = nullptr;
   HIP_OK(hipMalloc(&ws, ws_bytes));
 
-  int rc = co_alibi_fwd(dtype, q.p, k.p, v.p, (const float*)sl.p, o.p, (float*)lse.p, (float*)zb.p, B, Hq, Hkv, Sq,
+  int rc = co_alibi_fwd(dtype, q.p, k.p, v.p, (const float*)sl.p, o.p, (float*)lse.p, (float*)stats.p, B, Hq, Hkv, Sq,
                         Skv, D, causal, (float)scale, stream);
   if (rc == CO_ALIBI_OK)
-    rc = co_alibi_bwd(dtype, dout.p, q.p, k.p, v.p, o.p, (const float*)lse.p, (const float*)zb.p,
+    rc = co_alibi_bwd(dtype, dout.p, q.p, k.p, v.p, o.p, (const float*)lse.p, (const float*)stats.p,
                       (const float*)sl.p, dq.p, dk.p, dv.p, ws, ws_bytes, B, Hq, Hkv, Sq, Skv, D, causal,
                       (float)scale, stream);
   HIP_OK(hipStreamSynchronize(stream));
@@ -227,7 +227,7 @@ void check_errors(hipStream_t stream) {
                                     (const float*)sl.p, o.p, o.p, o.p, ws.p, 0, 1, 2, 2, 8, 8, 64, 1, 0.125f, stream);
   expect("error: a workspace of 0 bytes is EINVAL", small_ws == CO_ALIBI_EINVAL &&
                                                         std::strstr(co_alibi_last_error(), "workspace") != nullptr);
-  expect("abi version 5", co_alibi_abi_version() == 5);
+  expect("abi version 6", co_alibi_abi_version() == 6);
 }
 
 }  // namespace

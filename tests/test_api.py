@@ -26,19 +26,39 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in co_alibi.h but not exported"
     assert sorted(_native.EXPORTS) == declared
-    assert lib.co_alibi_abi_version() == 5
+    assert lib.co_alibi_abi_version() == _native.ABI_VERSION == 6
 
 
 def test_sizes():
     lib = _native.lib()
-    # zb: B*Hq * (ceil(Skv/32)*Sq blocks + ceil(Sq/128) kstart + ceil(Skv/256) key-norm chunks)
-    # zb blocks, kstart, knorm, then the row and key work orders
-    assert lib.co_alibi_zb_numel(4, 16, 4096, 4096) == 4 * 16 * (128 * 4096 + 32 + 16 + 32 + 64)
-    assert lib.co_alibi_zb_numel(1, 2, 5, 33) == 1 * 2 * (2 * 5 + 1 + 1 + 1 + 1)
-    assert lib.co_alibi_zb_numel(0, 2, 5, 33) == 0
+    # stats: a 4-word header, then B*Hq * (ceil(Sq/128) kstart + ceil(Skv/256) key-norm chunks +
+    # ceil(Sq/128) row order + ceil(Skv/64) key order + 2*Sq row sigmoid sums): O(B*Hq*S), no
+    # per-block penalty sums
+    assert lib.co_alibi_stats_numel(4, 16, 4096, 4096) == 4 + 4 * 16 * (32 + 16 + 32 + 64 + 2 * 4096)
+    assert lib.co_alibi_stats_numel(1, 2, 5, 33) == 4 + 1 * 2 * (1 + 1 + 1 + 1 + 10)
+    assert lib.co_alibi_stats_numel(1, 8, 65536, 65536) == 4 + 8 * (512 + 256 + 512 + 1024 + 2 * 65536)
+    assert lib.co_alibi_stats_numel(0, 2, 5, 33) == 0
+    # the recompute path's workspace: dO.O per row, then zb and cb (each 256-byte rounded)
     rows = 4 * 16 * 4096
-    assert lib.co_alibi_bwd_workspace_bytes(4, 16, 4096, 4096) == rows * 4 + 4 * 16 * 128 * 4096 * 4
-    assert lib.co_alibi_bwd_workspace_bytes(1, 1, 3, 3) == 256 + 1 * 1 * 1 * 3 * 4
+    assert lib.co_alibi_bwd_workspace_bytes(4, 16, 4096, 4096) == rows * 4 + 2 * 4 * 16 * 128 * 4096 * 4
+    assert lib.co_alibi_bwd_workspace_bytes(1, 1, 3, 3) == 256 + 2 * 256
+
+
+def test_tail_skip_setting():
+    """The library's tail-skip setting: on by default, returned by each set call, restored by the
+    context manager (no GPU call is involved)."""
+    lib = _native.lib()
+    assert lib.co_alibi_tail_skip() == 1
+    assert lib.co_alibi_set_tail_skip(0) == 1
+    assert lib.co_alibi_tail_skip() == 0
+    assert lib.co_alibi_set_tail_skip(5) == 0  # any non-zero value turns it on
+    assert lib.co_alibi_tail_skip() == 1
+    with _native.tail_skip(False):
+        assert lib.co_alibi_tail_skip() == 0
+        with _native.tail_skip(True):
+            assert lib.co_alibi_tail_skip() == 1
+        assert lib.co_alibi_tail_skip() == 0
+    assert lib.co_alibi_tail_skip() == 1
 
 
 def test_score_store_sizes():
@@ -66,11 +86,11 @@ def test_score_store_sizes():
 
 
 def _fwd(lib, **over):
-    args = dict(dtype=1, q=16, k=16, v=16, slopes=16, o=16, lse=16, zb=16, B=1, Hq=2, Hkv=2, Sq=8, Skv=8,
+    args = dict(dtype=1, q=16, k=16, v=16, slopes=16, o=16, lse=16, stats=16, B=1, Hq=2, Hkv=2, Sq=8, Skv=8,
                 D=64, causal=1, scale=0.125)
     args.update(over)
     return lib.co_alibi_fwd(args["dtype"], args["q"], args["k"], args["v"], args["slopes"], args["o"],
-                            args["lse"], args["zb"], args["B"], args["Hq"], args["Hkv"], args["Sq"],
+                            args["lse"], args["stats"], args["B"], args["Hq"], args["Hkv"], args["Sq"],
                             args["Skv"], args["D"], args["causal"], args["scale"], None)
 
 

@@ -35,18 +35,15 @@ def test_opcheck_fwd_bwd(dtype):
     sl, scale = slopes(4, dtype), 1 / 8
     grads = tuple(t.clone().requires_grad_() for t in (q, k, v))
     torch.library.opcheck(torch.ops.co_alibi.fwd, (q, k, v, sl, True, scale, False))
-    # Non-causal at a length the tail skip does not shorten: every entry of zb (and of its
-    # kstart / knorm tails) is written, so eager and AOT-traced outputs compare in full.
+    # With the tail skip on, every word of the saved statistics is written (header, kstart, key
+    # norms, work orders), so eager and AOT-traced outputs compare in full, causal or not.
     torch.library.opcheck(torch.ops.co_alibi.fwd, (*grads, sl, False, scale, True))
-    # Causal: zb entries past the diagonal are unwritten (nothing reads them), so the
-    # eager-vs-traced output comparison is left to test_compile_fullgraph_matches_eager.
-    torch.library.opcheck(torch.ops.co_alibi.fwd, (*grads, sl, True, scale, True),
-                          test_utils=("test_schema", "test_autograd_registration", "test_faketensor"))
-    o, lse, zb = torch.ops.co_alibi.fwd(q, k, v, sl, True, scale, True)
-    torch.library.opcheck(torch.ops.co_alibi.bwd, (do, q, k, v, o, lse, zb, sl, True, scale))
-    torch.library.opcheck(torch.ops.co_alibi.bwd_dq, (do, q, k, v, o, lse, zb, sl, True, scale))
-    dq_full = torch.ops.co_alibi.bwd(do, q, k, v, o, lse, zb, sl, True, scale)[0]
-    assert torch.equal(torch.ops.co_alibi.bwd_dq(do, q, k, v, o, lse, zb, sl, True, scale), dq_full)
+    torch.library.opcheck(torch.ops.co_alibi.fwd, (*grads, sl, True, scale, True))
+    o, lse, stats = torch.ops.co_alibi.fwd(q, k, v, sl, True, scale, True)
+    torch.library.opcheck(torch.ops.co_alibi.bwd, (do, q, k, v, o, lse, stats, sl, True, scale))
+    torch.library.opcheck(torch.ops.co_alibi.bwd_dq, (do, q, k, v, o, lse, stats, sl, True, scale))
+    dq_full = torch.ops.co_alibi.bwd(do, q, k, v, o, lse, stats, sl, True, scale)[0]
+    assert torch.equal(torch.ops.co_alibi.bwd_dq(do, q, k, v, o, lse, stats, sl, True, scale), dq_full)
 
 
 def test_opcheck_decode():
@@ -95,8 +92,8 @@ def test_graph_capture_replays_match_eager():
     qd = q[:, :, -1:].clone()
 
     def work():
-        o, lse, zb = torch.ops.co_alibi.fwd(q, k, v, sl, True, scale, True)
-        dq, dk, dv = torch.ops.co_alibi.bwd(do, q, k, v, o, lse, zb, sl, True, scale)
+        o, lse, stats = torch.ops.co_alibi.fwd(q, k, v, sl, True, scale, True)
+        dq, dk, dv = torch.ops.co_alibi.bwd(do, q, k, v, o, lse, stats, sl, True, scale)
         od, lsed = torch.ops.co_alibi.decode(qd, k, v, sl, None, S, scale, True)
         return o, lse, dq, dk, dv, od, lsed
 

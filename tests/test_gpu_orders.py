@@ -1,11 +1,12 @@
 """Work orders of the tail skip (coalibi_kernels.h).  The forward's key-norm launch writes, into
-the zb tail, the order in which the forward and backward pass 1 take their 128-row blocks and,
-with one query head per key head, the order of pass 2's 64-key blocks (the index order else);
-the inference forward writes the row order into its workspace.  Each order must be a
-permutation of its grid's items, so that every block is processed exactly once, and it must
-equal the stable descending sort of the predicted costs, restated here in numpy.  Every
-element of the zb tail is written (the zb buffer is an output).  The kernels' results do not
-depend on the order (the parity tests cover them).  Needs an MI355X.
+the saved statistics, the order in which the forward and backward pass 1 take their 128-row
+blocks and, with one query head per key head, the order of pass 2's 64-key blocks (the index
+order else); the inference forward writes the row order into its workspace.  Each order must be
+a permutation of its grid's items, so that every block is processed exactly once, and it must
+equal the stable descending sort of the predicted costs, restated here in numpy.  The
+statistics' header flags which tables the backward may follow.  With the tail skip switched
+off no table is written or flagged and every kstart is 0.  The kernels' results do not depend
+on the order (the parity tests cover them).  Needs an MI355X.
 """
 import math
 
@@ -62,7 +63,7 @@ def key_order(slopes, B, H, Sq, Skv, causal, dtype):
     return stable_desc(buckets_of(capped(rows, slopes[bh % H], window(dtype)), Sq))
 
 
-def run_fwd(B, Hq, Hkv, Sq, Skv, D, dtype, causal, slopes):
+def run_fwd(B, Hq, Hkv, Sq, Skv, D, dtype, causal, slopes, skip=True):
     lib = _native.lib()
     g = torch.Generator().manual_seed(1)
     q, k, v = ((torch.randn(B, h, s, D, generator=g) * 0.5).to(dtype).to(DEV)
@@ -70,19 +71,21 @@ def run_fwd(B, Hq, Hkv, Sq, Skv, D, dtype, causal, slopes):
     lam = torch.tensor(slopes, dtype=torch.float32, device=DEV)
     o = torch.empty_like(q)
     lse = torch.empty(B, Hq, Sq, device=DEV)
-    zb = torch.full((lib.co_alibi_zb_numel(B, Hq, Sq, Skv),), -1.0, device=DEV)
+    stats = torch.full((lib.co_alibi_stats_numel(B, Hq, Sq, Skv),), -1.0, device=DEV)
     st = torch.cuda.current_stream().cuda_stream
-    _native.check(lib.co_alibi_fwd(_native.DTYPE_CODES[dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                   lam.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), B, Hq, Hkv, Sq,
-                                   Skv, D, int(causal), 1.0 / math.sqrt(D), st))
     ws_bytes = lib.co_alibi_fwd_inference_workspace_bytes(B, Hq, Sq, Skv)
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=DEV)
     o_inf = torch.empty_like(q)
-    _native.check(lib.co_alibi_fwd_inference(_native.DTYPE_CODES[dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                             lam.data_ptr(), o_inf.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq, Hkv,
-                                             Sq, Skv, D, int(causal), 1.0 / math.sqrt(D), st))
+    with _native.tail_skip(skip):
+        _native.check(lib.co_alibi_fwd(_native.DTYPE_CODES[dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                       lam.data_ptr(), o.data_ptr(), lse.data_ptr(), stats.data_ptr(), B, Hq, Hkv,
+                                       Sq, Skv, D, int(causal), 1.0 / math.sqrt(D), st))
+        _native.check(lib.co_alibi_fwd_inference(_native.DTYPE_CODES[dtype], q.data_ptr(), k.data_ptr(),
+                                                 v.data_ptr(), lam.data_ptr(), o_inf.data_ptr(), ws.data_ptr(),
+                                                 ws_bytes, B, Hq, Hkv, Sq, Skv, D, int(causal), 1.0 / math.sqrt(D),
+                                                 st))
     torch.cuda.synchronize()
-    return zb.cpu(), ws.cpu(), o.cpu(), o_inf.cpu()
+    return stats.cpu(), ws.cpu(), o.cpu(), o_inf.cpu()
 
 
 CASES = [
@@ -103,10 +106,12 @@ def test_orders_are_sorted_permutations(case):
         slopes = (2.0 * _get_coalibi_slopes(Hq, 8.0)).to(dtype).float().numpy()
     else:
         slopes = np.array(sl, dtype=np.float32)
-    zb, ws, o, o_inf = run_fwd(B, Hq, Hkv, Sq, Skv, D, dtype, causal, slopes.tolist())
+    stats, ws, o, o_inf = run_fwd(B, Hq, Hkv, Sq, Skv, D, dtype, causal, slopes.tolist())
     bh, nqb, nkc, nkb = B * Hq, -(-Sq // 128), -(-Skv // 256), -(-Skv // 64)
-    tail = bh * -(-Skv // 32) * Sq + bh * (nqb + nkc)
-    ints = zb.view(torch.int32).numpy()
+    ints = stats.view(torch.int32).numpy()
+    # header: the row table and, with one query head per key head, the key table are flagged
+    assert ints[0] == 1 | (2 if Hq == Hkv else 0) and not ints[1:4].any()
+    tail = 4 + bh * (nqb + nkc)
     rows = ints[tail: tail + bh * nqb]
     assert np.array_equal(np.sort(rows), np.arange(bh * nqb)), "row order is not a permutation"
     assert np.array_equal(rows, row_order(slopes, B, Hq, Sq, Skv, causal, dtype))
@@ -121,4 +126,19 @@ def test_orders_are_sorted_permutations(case):
     # The inference forward: the same row order after its key-norm floats, and the same output.
     inf_rows = ws.view(torch.int32).numpy()[B * Hq * nkc: B * Hq * nkc + bh * nqb]
     assert np.array_equal(inf_rows, rows)
+    assert torch.equal(o, o_inf)
+
+
+@pytest.mark.parametrize("case", CASES[:2], ids=["mha", "gqa"])
+def test_no_tables_without_the_tail_skip(case):
+    """With the tail skip switched off the forward flags no work order (the backward then uses
+    its fixed orders), records kstart = 0 for every row block, and gives the same O as the
+    inference forward under the same setting."""
+    B, Hq, Hkv, Sq, Skv, D, dtype, causal, _ = case
+    slopes = (2.0 * _get_coalibi_slopes(Hq, 8.0)).to(dtype).float().numpy()
+    stats, _, o, o_inf = run_fwd(B, Hq, Hkv, Sq, Skv, D, dtype, causal, slopes.tolist(), skip=False)
+    ints = stats.view(torch.int32).numpy()
+    nqb = -(-Sq // 128)
+    assert not ints[:4].any()
+    assert not ints[4: 4 + B * Hq * nqb].any()
     assert torch.equal(o, o_inf)

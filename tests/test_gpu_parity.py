@@ -4,14 +4,13 @@ Bar: max-abs <= 1e-4 in the fp32 validation mode,
 <= 2e-2 for O, dQ, dK, dV with fp16/bf16 inputs, against the oracle run in
 fp32 on the same (dtype-rounded) inputs with the same dtype-rounded slopes.
 
-The bar is applied as written, with no allowance, to every output whose largest
-reference value is at most REF_SCALE[dtype].  Past that magnitude no kernel can
-meet an absolute bar: the output type's own rounding is up to half an ulp of the
-value, |x| 2^-9 in bf16 (already 2e-2 at |x| = 5.1) and |x| 2^-12 in fp16, and
-sums over many rows and grouped heads carry error relative to their size.  Such
-outputs (grouped-query dK/dV, non-causal sums, reaching 10-160 in the random
-sweeps) get the bar scaled by max|ref| / REF_SCALE[dtype]; the worst error as a
-share of its bar is printed per dtype at the end of the module.
+The bar is applied as written, with no allowance, to every fp32 output, and to every
+16-bit output whose largest reference value is at most REF_SCALE[dtype].  Past that
+magnitude no kernel can meet an absolute bar in a 16-bit output type: its own rounding
+is up to half an ulp of the value, |x| 2^-9 in bf16 (already 2e-2 at |x| = 5.1) and
+|x| 2^-12 in fp16.  Such outputs (grouped-query dK/dV, non-causal sums, reaching
+10-160 in the random sweeps) get the bar scaled by max|ref| / REF_SCALE[dtype].  The
+worst error as a share of its bar is printed per dtype at the end of the module.
 Every GPU call goes through the C ABI (directly, or via the drop-in API and the
 torch operators over it).
 """
@@ -59,13 +58,15 @@ def rand_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=0, scale=0.5):
     return q, k, v, do
 
 
-# Largest reference magnitude at which the absolute bar applies unchanged (see the module docstring).
-REF_SCALE = {torch.float32: 4.0, torch.float16: 16.0, torch.bfloat16: 4.0}
+# Largest reference magnitude at which the absolute bar applies unchanged (see the module docstring):
+# fp32 outputs carry no output rounding of that size, so their bar is never scaled.
+REF_SCALE = {torch.float32: math.inf, torch.float16: 16.0, torch.bfloat16: 4.0}
 WORST = {}  # dtype name -> (worst error / bar, label)
 
 
 def assert_parity(got, want, tol, label, dtype=torch.float32):
-    """max-abs <= tol for outputs up to REF_SCALE[dtype] in magnitude, tol * max|ref| / REF_SCALE beyond."""
+    """max-abs <= tol for outputs up to REF_SCALE[dtype] in magnitude, tol * max|ref| / REF_SCALE beyond
+    (16-bit types only)."""
     for name, g, w in zip(("o", "dq", "dk", "dv"), got, want):
         assert torch.isfinite(g).all(), f"{label}: {name} has non-finite values"
         w = w.float()
@@ -88,17 +89,17 @@ def _report_worst_ratio():
 
 
 def hip_fwd_raw(q, k, v, slopes, causal, sm_scale):
-    """co_alibi_fwd through the C ABI; returns (o, lse, zb) on the device."""
+    """co_alibi_fwd through the C ABI; returns (o, lse, stats) on the device."""
     lib = _native.lib()
     B, Hq, Sq, D = q.shape
     Hkv, Skv = k.shape[1], k.shape[2]
     o = torch.empty_like(q)
     lse = torch.empty(B, Hq, Sq, device=DEV, dtype=torch.float32)
-    zb = torch.empty(lib.co_alibi_zb_numel(B, Hq, Sq, Skv), device=DEV, dtype=torch.float32)
+    stats = torch.empty(lib.co_alibi_stats_numel(B, Hq, Sq, Skv), device=DEV, dtype=torch.float32)
     _native.check(lib.co_alibi_fwd(_native.DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                   slopes.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), B, Hq, Hkv,
+                                   slopes.data_ptr(), o.data_ptr(), lse.data_ptr(), stats.data_ptr(), B, Hq, Hkv,
                                    Sq, Skv, D, int(causal), sm_scale, torch.cuda.current_stream().cuda_stream))
-    return o, lse, zb
+    return o, lse, stats
 
 
 # --------------------------------------------------------------------------- small shapes
@@ -159,25 +160,54 @@ def test_small_shapes(case, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
 def test_lse_and_penalty_statistics(dtype):
-    """LSE (natural log, m + log(l + 1e-9)) and zb (suffix sigmoid sums at 32-key block starts)."""
+    """LSE (natural log, m + log(l + 1e-9)); the row sigmoid sums R the forward saves (hi + lo);
+    and what backward pass 1 rebuilds from them while it walks each row's keys left to right,
+    read from the recompute path's workspace: zb[J][i] = sum of sigma_ik over k >= 32J and
+    cb[J][i] = sum of dA_ik over k < 32J, against the oracle's per-pair terms.  Also the saved
+    statistics' O(B*Hq*S) size and kstart = 0 (the slopes here are too flat to skip anything)."""
+    lib = _native.lib()
     B, Hq, Hkv, S, D = 1, 2, 2, 150, 64
-    q, k, v, _ = rand_inputs(B, Hq, Hkv, S, S, D, dtype, seed=2)
+    q, k, v, do = rand_inputs(B, Hq, Hkv, S, S, D, dtype, seed=2)
     lam = ref.slopes(Hq, dtype=dtype).float()
     scale = 1.0 / math.sqrt(D)
-    o, lse, zb = hip_fwd_raw(q.to(DEV), k.to(DEV), v.to(DEV), lam.to(DEV), True, scale)
+    qd, kd, vd, dod, lamd = (t.to(DEV) for t in (q, k, v, do, lam))
+    o, lse, stats = hip_fwd_raw(qd, kd, vd, lamd, True, scale)
+    ws_bytes = lib.co_alibi_bwd_workspace_bytes(B, Hq, S, S)
+    ws = torch.zeros(ws_bytes, device=DEV, dtype=torch.uint8)
+    dq = torch.empty_like(qd)
+    _native.check(lib.co_alibi_bwd_dq(_native.DTYPE_CODES[dtype], dod.data_ptr(), qd.data_ptr(), kd.data_ptr(),
+                                      vd.data_ptr(), o.data_ptr(), lse.data_ptr(), stats.data_ptr(),
+                                      lamd.data_ptr(), dq.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq, Hkv, S, S, D,
+                                      1, scale, torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
     _, lse_ref = ref.forward(q.float(), k.float(), v.float(), lam, causal=True, scale=scale)
     tol = 1e-4 if dtype == torch.float32 else 5e-3
     assert (lse.cpu() - lse_ref).abs().max().item() <= tol
+    nqb, nkc, nkb = (S + 127) // 128, (S + 255) // 256, (S + 63) // 64
+    assert stats.numel() == 4 + B * Hq * (2 * nqb + nkc + nkb + 2 * S)
+    st = stats.cpu()
+    assert not st[4:4 + B * Hq * nqb].view(torch.int32).any(), "kstart of flat slopes is 0"
+    r0 = 4 + B * Hq * (2 * nqb + nkc + nkb)
+    rsum = (st[r0:r0 + B * Hq * S].double() + st[r0 + B * Hq * S:r0 + 2 * B * Hq * S].double()).view(B * Hq, S)
     nzb = (S + 31) // 32
-    zb = zb[:B * Hq * nzb * S].view(B * Hq, nzb, S).cpu()  # the blocks proper, before the kstart / knorm tails
+    rows_bytes = (B * Hq * S * 4 + 255) // 256 * 256
+    blk_bytes = (B * Hq * nzb * S * 4 + 255) // 256 * 256
+    wsf = ws.cpu()
+    zb = wsf[rows_bytes:rows_bytes + B * Hq * nzb * S * 4].view(torch.float32).view(B * Hq, nzb, S)
+    cb = wsf[rows_bytes + blk_bytes:rows_bytes + blk_bytes + B * Hq * nzb * S * 4].view(torch.float32)
+    cb = cb.view(B * Hq, nzb, S)
     for h in range(Hq):
-        _, _, _, sig, _ = ref._rows_forward(q[0, h].float(), k[0, h].float(), v[0, h].float(), lam[h], True, scale, 0)
+        _, sig, da, _ = ref._rows_terms(q[0, h].float(), do[0, h].float(), k[0, h].float(), v[0, h].float(), lam[h],
+                                        True, scale, 0)
+        assert (rsum[h] - sig.double().sum(-1)).abs().max().item() <= 1e-5 * S
         suffix = torch.cumsum(sig.flip(-1), -1).flip(-1)  # [i, j] = sum_{k >= j} sigma_ik
+        prefix = torch.cumsum(da, -1) - da                # [i, j] = sum_{k < j} dA_ik
         for J in range(nzb):
-            rows = torch.arange(32 * J, S)  # rows that see key 32*J
-            err = (zb[h, J, rows] - suffix[rows, 32 * J]).abs().max().item()
-            assert err <= 1e-3 * max(1.0, S / 32), f"zb head {h} block {J}: {err}"
+            rows = torch.arange(32 * J, S)  # rows whose 32-row block processes key block J
+            err_z = (zb[h, J, rows] - suffix[rows, 32 * J]).abs().max().item()
+            err_c = (cb[h, J, rows] - prefix[rows, 32 * J]).abs().max().item()
+            assert err_z <= 1e-4 * max(1.0, S / 32), f"zb head {h} block {J}: {err_z}"
+            assert err_c <= (1e-5 if dtype == torch.float32 else 2e-3), f"cb head {h} block {J}: {err_c}"
 
 
 @pytest.mark.parametrize("path", PATHS)
@@ -189,7 +219,7 @@ def test_split_backward_equals_full(path):
     q, k, v, do = (t.to(DEV) for t in rand_inputs(B, Hq, Hkv, S, S, D, dtype, seed=3))
     lam = ref.slopes(Hq, dtype=dtype).float().to(DEV)
     scale = 1.0 / math.sqrt(D)
-    o, lse, zb = hip_fwd_raw(q, k, v, lam, True, scale)
+    o, lse, stats = hip_fwd_raw(q, k, v, lam, True, scale)
     ws_bytes = bwd_workspace_bytes(lib, path, dtype, B, Hq, Hkv, S, S, D, True)
     st = torch.cuda.current_stream().cuda_stream
     outs = []
@@ -199,14 +229,15 @@ def test_split_backward_equals_full(path):
         common = (B, Hq, Hkv, S, S, D, 1, scale, st)
         if split:
             _native.check(lib.co_alibi_bwd_dq(1, do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                                              lse.data_ptr(), zb.data_ptr(), lam.data_ptr(), dq.data_ptr(),
+                                              lse.data_ptr(), stats.data_ptr(), lam.data_ptr(), dq.data_ptr(),
                                               ws.data_ptr(), ws_bytes, *common))
             _native.check(lib.co_alibi_bwd_dkdv(1, do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                                lse.data_ptr(), zb.data_ptr(), lam.data_ptr(), dk.data_ptr(),
+                                                lse.data_ptr(), stats.data_ptr(), lam.data_ptr(), dk.data_ptr(),
                                                 dv.data_ptr(), ws.data_ptr(), ws_bytes, *common))
         else:
             _native.check(lib.co_alibi_bwd(1, do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                                           lse.data_ptr(), zb.data_ptr(), lam.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                                           lse.data_ptr(), stats.data_ptr(), lam.data_ptr(), dq.data_ptr(),
+                                           dk.data_ptr(),
                                            dv.data_ptr(), ws.data_ptr(), ws_bytes, *common))
         torch.cuda.synchronize()
         outs.append((dq.cpu(), dk.cpu(), dv.cpu()))
@@ -224,7 +255,7 @@ def test_repeat_call_deterministic():
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["fp16", "bf16", "fp32"])
 def test_inference_forward_equals_training_forward(dtype):
-    """Without gradients the forward writes no LSE / zb and returns bit-identical O (drop-in API
+    """Without gradients the forward writes no LSE / statistics and returns bit-identical O (drop-in API
     under no_grad, with inputs that need no grad: co_alibi_fwd_inference, whose tail skip takes
     the same decisions as the training forward's).  co_alibi_fwd with NULL statistics skips
     nothing: equal in fp16 (every skipped weight rounds to zero in P), within 1e-6 otherwise."""
@@ -267,7 +298,7 @@ def test_tail_skip(dtype, causal, path):
     """Slopes large enough that the forward stops early (keys whose weight is below 2^-26 (fp16),
     2^-32 (bf16) or 2^-64 (fp32) of their row's total are left out, and the backward passes
     leave out the same keys):
-    - the first processed key per 128-row block (the zb tail) is a multiple of 64, positive for
+    - the first processed key per 128-row block (in the statistics) is a multiple of 64, positive for
       the steep heads, zero for the flat one, and no later than the block's diagonal tile;
     - O equals the forward without statistics, which skips nothing (bit for bit in fp16,
       where each skipped weight rounds to zero; within 1e-6 in bf16 and fp32);
@@ -275,16 +306,18 @@ def test_tail_skip(dtype, causal, path):
     lib = _native.lib()
     B, Hq, Hkv, S, D = 1, 4, 2, 1000, 64
     q, k, v, do = rand_inputs(B, Hq, Hkv, S, S, D, dtype, seed=21)
-    # Steep slopes concentrate each row's weight on a few keys, so dV_k is close to a few dO
-    # rows; dO at half scale keeps |dV| within the range where the bar applies unscaled.
-    do = (do.float() * 0.5).to(dtype)
+    # Steep slopes concentrate each row's weight on a few keys: causal, dV_k is close to a few dO
+    # rows; non-causal, every row weighs the last keys, so their dV sums all 1000 rows.  dO is
+    # scaled so that |dV| stays within the range where the bar applies unscaled (in fp32 the
+    # arithmetic's own rounding, the oracle's included, reaches 1e-4 at |dV| ~ 30 with slope 4).
+    do = (do.float() * (0.5 if causal else 0.05)).to(dtype)
     lam = torch.tensor([4.0, 1.0, 0.25, 1e-3]).to(dtype).float()
     scale = 1.0 / math.sqrt(D)
     if path == "store" and dtype == torch.float32:
         pytest.skip("the score store is a 16-bit path")
     print(f"tail skip {dtype} causal={causal} {path}", flush=True)
     qd, kd, vd, dod, lamd = (t.to(DEV) for t in (q, k, v, do, lam))
-    o, lse, zb = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
+    o, lse, stats = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
     st = torch.cuda.current_stream().cuda_stream
     o_plain = torch.empty_like(qd)
     _native.check(lib.co_alibi_fwd(_native.DTYPE_CODES[dtype], qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
@@ -294,12 +327,12 @@ def test_tail_skip(dtype, causal, path):
     ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
     dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
     _native.check(lib.co_alibi_bwd(_native.DTYPE_CODES[dtype], dod.data_ptr(), qd.data_ptr(), kd.data_ptr(),
-                                   vd.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), lamd.data_ptr(),
+                                   vd.data_ptr(), o.data_ptr(), lse.data_ptr(), stats.data_ptr(), lamd.data_ptr(),
                                    dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq, Hkv,
                                    S, S, D, int(causal), scale, st))
     torch.cuda.synchronize()
-    nzb, nqb = (S + 31) // 32, (S + 127) // 128
-    kstart = zb[B * Hq * nzb * S:B * Hq * (nzb * S + nqb)].view(torch.int32).view(Hq, nqb).cpu()
+    nqb = (S + 127) // 128
+    kstart = stats[4:4 + B * Hq * nqb].view(torch.int32).view(Hq, nqb).cpu()
     print(f"  first processed key per 128-row block:\n{kstart}", flush=True)
     assert (kstart % 64 == 0).all() and (kstart >= 0).all()
     last_tile = torch.tensor([(min(qb * 128 + 127, S - 1) if causal else S - 1) // 64 * 64 for qb in range(nqb)])
@@ -313,6 +346,58 @@ def test_tail_skip(dtype, causal, path):
     rdq, rdk, rdv = ref.backward(do.float(), q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
     assert_parity(tuple(t.float().cpu() for t in (o, dq, dk, dv)), (ro, rdq, rdk, rdv), TOL[dtype],
                   f"tail skip causal={causal} {path}", dtype)
+
+
+def _fwd_bwd_raw(qd, kd, vd, dod, lamd, causal, scale, path, skip):
+    """co_alibi_fwd then co_alibi_bwd through the C ABI under the given tail-skip setting; returns
+    (o, dq, dk, dv, kstart) on the CPU."""
+    lib = _native.lib()
+    B, Hq, Sq, D = qd.shape
+    Hkv, Skv = kd.shape[1], kd.shape[2]
+    dtype = qd.dtype
+    with _native.tail_skip(skip):
+        o, lse, stats = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
+    ws_bytes = bwd_workspace_bytes(lib, path, dtype, B, Hq, Hkv, Sq, Skv, D, causal)
+    ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    _native.check(lib.co_alibi_bwd(_native.DTYPE_CODES[dtype], dod.data_ptr(), qd.data_ptr(), kd.data_ptr(),
+                                   vd.data_ptr(), o.data_ptr(), lse.data_ptr(), stats.data_ptr(), lamd.data_ptr(),
+                                   dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq, Hkv,
+                                   Sq, Skv, D, int(causal), scale, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    nqb = (Sq + 127) // 128
+    kstart = stats[4:4 + B * Hq * nqb].view(torch.int32).view(B * Hq, nqb).cpu()
+    return tuple(t.float().cpu() for t in (o, dq, dk, dv)) + (kstart,)
+
+
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["fp16", "bf16", "fp32"])
+def test_tail_skip_backward_matches_full_work(dtype, path):
+    """The backward with the tail skip against the same backward with the skip switched off (every
+    key processed, kstart = 0), on slopes steep enough to skip most keys.  A skipped pair has
+    s < 2^-T (T = 26, 32, 64 for fp16, bf16, fp32), so its dA = s (dS - D) and its share of the
+    prefix C are below 2^-T of the row's scale, and the gradients' fp32 accumulators differ by
+    far less than one rounding step of the output type.  The bound: one unit in the last place
+    of the output type at the output's largest magnitude (16-bit), or 1e-6 of it (fp32)."""
+    if path == "store" and dtype == torch.float32:
+        pytest.skip("the score store is a 16-bit path")
+    B, Hq, Hkv, S, D = 1, 4, 2, 1000, 64
+    q, k, v, do = rand_inputs(B, Hq, Hkv, S, S, D, dtype, seed=21)
+    do = (do.float() * 0.5).to(dtype)
+    lam = torch.tensor([4.0, 1.0, 0.25, 1e-3]).to(dtype).float()
+    scale = 1.0 / math.sqrt(D)
+    print(f"skipped vs full-work backward {dtype} {path}", flush=True)
+    qd, kd, vd, dod, lamd = (t.to(DEV) for t in (q, k, v, do, lam))
+    got = _fwd_bwd_raw(qd, kd, vd, dod, lamd, True, scale, path, skip=True)
+    full = _fwd_bwd_raw(qd, kd, vd, dod, lamd, True, scale, path, skip=False)
+    assert (got[4][0] > 0).sum() >= 6 and not full[4].any(), "the steep head skips; the full run skips nothing"
+    mant = {torch.float16: 10, torch.bfloat16: 7}
+    for name, a, b in zip(("o", "dq", "dk", "dv"), got[:4], full[:4]):
+        top = max(b.abs().max().item(), 1e-30)
+        bound = 2.0 ** (math.floor(math.log2(top)) - mant[dtype]) if dtype in mant else 1e-6 * top
+        err = (a - b).abs().max().item()
+        print(f"  {name}: skipped vs full work {err:.3e} (bound {bound:.3e})", flush=True)
+        assert err <= bound, f"{name}: {err} > {bound}"
 
 
 @pytest.mark.parametrize("path", PATHS)
@@ -330,18 +415,18 @@ def test_tail_skip_grouped_rectangular(dtype, causal, path):
     scale = 1.0 / math.sqrt(D)
     print(f"tail skip grouped {dtype} causal={causal} {path}", flush=True)
     qd, kd, vd, dod, lamd = (t.to(DEV) for t in (q, k, v, do, lam))
-    o, lse, zb = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
+    o, lse, stats = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
     st = torch.cuda.current_stream().cuda_stream
     ws_bytes = bwd_workspace_bytes(lib, path, dtype, B, Hq, Hkv, Sq, Skv, D, causal)
     ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
     dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
     _native.check(lib.co_alibi_bwd(_native.DTYPE_CODES[dtype], dod.data_ptr(), qd.data_ptr(), kd.data_ptr(),
-                                   vd.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), lamd.data_ptr(),
+                                   vd.data_ptr(), o.data_ptr(), lse.data_ptr(), stats.data_ptr(), lamd.data_ptr(),
                                    dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq, Hkv,
                                    Sq, Skv, D, int(causal), scale, st))
     torch.cuda.synchronize()
-    nzb, nqb = (Skv + 31) // 32, (Sq + 127) // 128
-    kstart = zb[B * Hq * nzb * Sq:B * Hq * (nzb * Sq + nqb)].view(torch.int32).view(B, Hq, nqb).cpu()
+    nqb = (Sq + 127) // 128
+    kstart = stats[4:4 + B * Hq * nqb].view(torch.int32).view(B, Hq, nqb).cpu()
     assert (kstart[:, 0].max() > 0) and (kstart[:, 4] == 0).all()  # the steep head skips, the flattest does not
     ro, _ = ref.forward(q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
     rdq, rdk, rdv = ref.backward(do.float(), q.float(), k.float(), v.float(), lam, causal=causal, scale=scale)
@@ -373,7 +458,7 @@ def test_score_store_matches_recompute(case, dtype):
     scale = 1.0 / math.sqrt(D)
     print(f"score store {case} {dtype}", flush=True)
     qd, kd, vd, dod, lamd = (t.to(DEV) for t in (q, k, v, do, lam))
-    o, lse, zb = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
+    o, lse, stats = hip_fwd_raw(qd, kd, vd, lamd, causal, scale)
     st = torch.cuda.current_stream().cuda_stream
     outs = {}
     for path in PATHS:
@@ -381,7 +466,7 @@ def test_score_store_matches_recompute(case, dtype):
         ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
         dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
         _native.check(lib.co_alibi_bwd(_native.DTYPE_CODES[dtype], dod.data_ptr(), qd.data_ptr(), kd.data_ptr(),
-                                       vd.data_ptr(), o.data_ptr(), lse.data_ptr(), zb.data_ptr(), lamd.data_ptr(),
+                                       vd.data_ptr(), o.data_ptr(), lse.data_ptr(), stats.data_ptr(), lamd.data_ptr(),
                                        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq,
                                        Hkv, Sq, Skv, D, int(causal), scale, st))
         torch.cuda.synchronize()
@@ -476,27 +561,34 @@ FULL = ("headline", "gqa", "long")
 @pytest.mark.parametrize("name", FULL)
 def test_full_size_config(name):
     """BASELINE configs[1..3] at full size: every (batch, query head) of O and dQ and every
-    (batch, key head) of dK and dV against the chunked CPU oracle, with the bar of assert_parity."""
+    (batch, key head) of dK and dV against the chunked CPU oracle, with the bar of assert_parity,
+    both with the tail skip (the default) and with it switched off (every key processed, as the
+    reference's kernels do; the mode the full-work measurements run in)."""
     w = WORKLOADS[name]
     print(f"config {name}: B{w.batch} Hq{w.heads_q} Hkv{w.heads_kv} S{w.seq} D{w.head_dim} {w.dtype}", flush=True)
     q, k, v, do = make_inputs(w, seed=0)
-    got = hip_fwd_bwd(q, k, v, do, causal=w.causal, bias_max=w.bias_max)
+    runs = {}
+    for skip in (True, False):
+        with _native.tail_skip(skip):
+            runs[skip] = hip_fwd_bwd(q, k, v, do, causal=w.causal, bias_max=w.bias_max)
     # Size-independent identity: sum over keys of dV = sum over rows of dO (weights sum to 1).
     g = w.heads_q // w.heads_kv
-    dv = got[3]
-    dv_sum = dv.double().sum(2)                                             # (B, Hkv, D)
     do_sum = do.double().view(w.batch, w.heads_kv, g, w.seq, w.head_dim).sum((2, 3))
-    rel = ((dv_sum - do_sum).abs().max() / do_sum.abs().max()).item()
-    print(f"  sum_j dV_j vs sum_i dO_i: rel {rel:.2e}", flush=True)
-    assert rel < 1e-2
+    for skip, got in runs.items():
+        dv_sum = got[3].double().sum(2)                                     # (B, Hkv, D)
+        rel = ((dv_sum - do_sum).abs().max() / do_sum.abs().max()).item()
+        print(f"  tail skip {skip}: sum_j dV_j vs sum_i dO_i: rel {rel:.2e}", flush=True)
+        assert rel < 1e-2
     ro, _, rdq, rdk, rdv = oracle_fwd_bwd(q, k, v, do, causal=w.causal, bias_max=w.bias_max)
-    # Per-head maxima, so a failure names its head.
-    for n_, a_, b_ in zip(("o", "dq", "dk", "dv"), got, (ro, rdq, rdk, rdv)):
-        per_head = (a_ - b_).abs().amax(dim=(2, 3))
-        b0, h0 = divmod(int(per_head.argmax()), per_head.shape[1])
-        print(f"  {name} {n_}: worst head (b{b0}, h{h0}) max-abs {per_head.max().item():.3e} over "
-              f"{per_head.numel()} heads", flush=True)
-    assert_parity(got, (ro, rdq, rdk, rdv), TOL[w.dtype], f"{name} (all heads)", w.dtype)
+    for skip, got in runs.items():
+        label = f"{name} (all heads, tail skip {'on' if skip else 'off'})"
+        # Per-head maxima, so a failure names its head.
+        for n_, a_, b_ in zip(("o", "dq", "dk", "dv"), got, (ro, rdq, rdk, rdv)):
+            per_head = (a_ - b_).abs().amax(dim=(2, 3))
+            b0, h0 = divmod(int(per_head.argmax()), per_head.shape[1])
+            print(f"  {label} {n_}: worst head (b{b0}, h{h0}) max-abs {per_head.max().item():.3e} over "
+                  f"{per_head.numel()} heads", flush=True)
+        assert_parity(got, (ro, rdq, rdk, rdv), TOL[w.dtype], label, w.dtype)
 
 
 @pytest.mark.parametrize("name", FULL)

@@ -18,11 +18,11 @@ def test_operators_are_registered_with_their_schemas():
     bwd = str(torch.ops.co_alibi.bwd.default._schema)
     dec = str(torch.ops.co_alibi.decode.default._schema)
     bwd_dq = str(torch.ops.co_alibi.bwd_dq.default._schema)
-    assert bwd_dq == ("co_alibi::bwd_dq(Tensor do, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor zb, "
+    assert bwd_dq == ("co_alibi::bwd_dq(Tensor do, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor stats, "
                       "Tensor slopes, bool causal, float sm_scale) -> Tensor")
     assert fwd == ("co_alibi::fwd(Tensor q, Tensor k, Tensor v, Tensor slopes, bool causal, float sm_scale, "
                    "bool with_stats) -> (Tensor, Tensor, Tensor)")
-    assert bwd == ("co_alibi::bwd(Tensor do, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor zb, "
+    assert bwd == ("co_alibi::bwd(Tensor do, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor stats, "
                    "Tensor slopes, bool causal, float sm_scale) -> (Tensor, Tensor, Tensor)")
     assert dec == ("co_alibi::decode(Tensor q, Tensor k_cache, Tensor v_cache, Tensor slopes, Tensor? seq_lens, "
                    "SymInt max_seq_len, float sm_scale, bool with_lse) -> (Tensor, Tensor)")
@@ -34,27 +34,27 @@ def test_fwd_fake_shapes(shape, dtype):
     B, Hq, Sq, Skv, D = shape
     Hkv = max(1, Hq // 4)
     q, k, v = meta(B, Hq, Sq, D, dtype=dtype), meta(B, Hkv, Skv, D, dtype=dtype), meta(B, Hkv, Skv, D, dtype=dtype)
-    o, lse, zb = torch.ops.co_alibi.fwd(q, k, v, meta(Hq, dtype=dtype), True, 0.1, True)
+    o, lse, stats = torch.ops.co_alibi.fwd(q, k, v, meta(Hq, dtype=dtype), True, 0.1, True)
     assert o.shape == q.shape and o.dtype == dtype and o.is_contiguous()
     assert lse.shape == (B, Hq, Sq) and lse.dtype == torch.float32
-    assert zb.shape == (ops.zb_numel(B, Hq, Sq, Skv),) and zb.dtype == torch.float32
-    o, lse, zb = torch.ops.co_alibi.fwd(q, k, v, meta(Hq, dtype=dtype), False, 0.1, False)
-    assert o.shape == q.shape and lse.numel() == 0 and zb.numel() == 0
+    assert stats.shape == (ops.stats_numel(B, Hq, Sq, Skv),) and stats.dtype == torch.float32
+    o, lse, stats = torch.ops.co_alibi.fwd(q, k, v, meta(Hq, dtype=dtype), False, 0.1, False)
+    assert o.shape == q.shape and lse.numel() == 0 and stats.numel() == 0
 
 
-def test_zb_numel_matches_the_library():
+def test_stats_numel_matches_the_library():
     lib = _native.lib()
     for args in [(1, 1, 1, 1), (4, 16, 4096, 4096), (1, 32, 8192, 8192), (2, 3, 100, 33), (1, 2, 5, 64)]:
-        assert ops.zb_numel(*args) == lib.co_alibi_zb_numel(*args)
+        assert ops.stats_numel(*args) == lib.co_alibi_stats_numel(*args)
 
 
 def test_fwd_autograd_reaches_bwd():
     """Backward of co_alibi::fwd is co_alibi::bwd: gradients of the input shapes and dtypes,
-    for grouped heads; lse and zb carry no gradient."""
+    for grouped heads; lse and stats carry no gradient."""
     B, Hq, Hkv, Sq, Skv, D = 2, 8, 2, 64, 96, 64
     q, k, v = meta(B, Hq, Sq, D, grad=True), meta(B, Hkv, Skv, D, grad=True), meta(B, Hkv, Skv, D, grad=True)
-    o, lse, zb = torch.ops.co_alibi.fwd(q, k, v, meta(Hq), True, 0.125, True)
-    assert o.requires_grad and not lse.requires_grad and not zb.requires_grad
+    o, lse, stats = torch.ops.co_alibi.fwd(q, k, v, meta(Hq), True, 0.125, True)
+    assert o.requires_grad and not lse.requires_grad and not stats.requires_grad
     o.float().sum().backward()
     for t in (q, k, v):
         assert t.grad.shape == t.shape and t.grad.dtype == t.dtype
@@ -96,7 +96,7 @@ def test_inference_forward_has_no_backward():
 def test_bwd_and_decode_fake_shapes():
     q, k = meta(2, 8, 50, 128, dtype=torch.bfloat16), meta(2, 2, 70, 128, dtype=torch.bfloat16)
     dq, dk, dv = torch.ops.co_alibi.bwd(q, q, k, k, q, meta(2, 8, 50, dtype=torch.float32),
-                                        meta(ops.zb_numel(2, 8, 50, 70), dtype=torch.float32),
+                                        meta(ops.stats_numel(2, 8, 50, 70), dtype=torch.float32),
                                         meta(8, dtype=torch.bfloat16), True, 0.1)
     assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape and dq.dtype == torch.bfloat16
     qd, cache = meta(3, 16, 1, 64), meta(3, 4, 1000, 64)

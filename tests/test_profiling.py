@@ -75,3 +75,88 @@ def test_attention_flops_closed_form():
     assert nc_fwd == 4 * 2 * 100 * 300 * 64 and nc_bwd == 2.5 * nc_fwd
     # one product of the per-kernel accounting is half the forward
     assert attention_flops(1, 1, 8, 8, 32, causal=True)[0] == 2 * (2 * 32 * 8 * 8 / 2)
+
+
+def _valid(ks, skv):
+    return ks if 0 <= ks <= skv else 0
+
+
+def _sim_rows(kernel, kstart, B, Hq, Sq, Skv, D, causal):
+    """The forward's / pass 1's loops, transcribed: per (head, 128-row block) the key tiles from the
+    diagonal one down to the recorded first processed key, per wavefront unless wholly above its rows."""
+    bn = 64 if kernel == "coalibi_fwd_kernel" else 32
+    KS, DT = D // 16, max(D, 32) // 32
+    per = 2 * KS + (4 if bn == 64 else 2) * DT
+    nqb, n = (Sq + 127) // 128, 0
+    for bh in range(B * Hq):
+        for qb in range(nqb):
+            q0 = qb * 128
+            last = min(q0 + 127, Skv - 1) if causal else Skv - 1
+            nkt = last // bn + 1
+            kt0 = _valid(int(kstart[bh][qb]), Skv) // bn
+            for kt in range(nkt - 1, kt0 - 1, -1):
+                for w in range(4):
+                    if causal and kt * bn > q0 + 32 * w + 31:
+                        continue
+                    n += per
+    return n
+
+
+def _sim_pass2(kernel, kstart, B, Hq, Hkv, Sq, Skv, D, causal):
+    """Pass 2's work list, transcribed: per key head and 64-key block, per query head of the group,
+    the 64-row tiles from the last one whose row block processed the block down to the first that
+    can see it; per wavefront (key group, query half) when that half holds a processed visible pair."""
+    KS, DT = D // 16, max(D, 32) // 32
+    per = 4 * DT + (2 * KS if kernel == "coalibi_bwd_dkdv_kernel" else 0)
+    g = Hq // Hkv
+    nqt, nrb, nkb, n = (Sq + 63) // 64, (Sq + 127) // 128, (Skv + 63) // 64, 0
+    for b in range(B):
+        for hkv in range(Hkv):
+            for kb in range(nkb):
+                kwg0 = kb * 64
+                qt0 = min(kwg0 // 64, nqt) if causal else 0
+                for gi in range(g):
+                    ks = kstart[b * Hq + hkv * g + gi]
+                    hi = qt0 - 1
+                    for rb in range(nrb):
+                        if _valid(int(ks[rb]), Skv) <= kwg0:
+                            hi = max(hi, min(2 * rb + 1, nqt - 1))
+                    for qt in range(hi, qt0 - 1, -1):
+                        processed = _valid(int(ks[qt // 2]), Skv) <= kwg0
+                        for kg in range(2):
+                            for qh in range(2):
+                                kw0, qs0 = kwg0 + 32 * kg, qt * 64 + 32 * qh
+                                if processed and kw0 < Skv and qs0 < Sq and (not causal or qs0 + 31 >= kw0):
+                                    n += per
+    return n
+
+
+def test_issued_products_match_the_kernel_loops():
+    """profiling.issued_k16 (vectorised) against the kernels' loops transcribed one by one, for
+    random recorded first keys (multiples of 64, and out-of-range values that the kernels read as
+    0), causal and not, square and rectangular, grouped heads; and the full-work forward at the
+    headline shape: every 64-key x 32-row tile at or below the diagonal."""
+    import numpy as np
+
+    rng = np.random.default_rng(7)
+    for (B, Hq, Hkv, Sq, Skv, D, causal) in [(1, 4, 2, 300, 300, 64, True), (2, 2, 2, 500, 260, 128, True),
+                                             (1, 3, 3, 200, 700, 32, False), (1, 2, 1, 1000, 1000, 16, True)]:
+        nqb = (Sq + 127) // 128
+        ks = rng.integers(0, (Skv + 63) // 64, size=(B * Hq, nqb)) * 64
+        ks[0, 0] = Skv + 5   # out of range: read as 0
+        ks[-1, -1] = -64
+        for kern in ("coalibi_fwd_kernel", "coalibi_bwd_dq_kernel"):
+            want = _sim_rows(kern, ks, B, Hq, Sq, Skv, D, causal)
+            assert profiling.issued_k16(kern, ks, B, Hq, Hkv, Sq, Skv, D, causal) == want, kern
+        for kern in ("coalibi_bwd_dkdv_store_kernel", "coalibi_bwd_dkdv_kernel"):
+            want = _sim_pass2(kern, ks, B, Hq, Hkv, Sq, Skv, D, causal)
+            assert profiling.issued_k16(kern, ks, B, Hq, Hkv, Sq, Skv, D, causal) == want, kern
+    # headline, nothing skipped: per (head, 128-row block qb), wavefront w processes tiles 0 ..
+    # (128 qb + 32 w + 31) // 64, each 2*8 + 4*4 = 32 products
+    zero = np.zeros((64, 32), dtype=np.int64)
+    per_head = sum(((128 * qb + 32 * w + 31) // 64 + 1) for qb in range(32) for w in range(4))
+    assert profiling.issued_k16("coalibi_fwd_kernel", zero, 4, 16, 16, 4096, 4096, 128) == 64 * per_head * 32
+    # ... which is the algorithmic causal forward plus the diagonal tiles' masked halves
+    fwd, _ = profiling.attention_flops(4, 16, 4096, 4096, 128)
+    issued = 64 * per_head * 32 * profiling.K16_FLOPS
+    assert 1.0 < issued / fwd < 1.03

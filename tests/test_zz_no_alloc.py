@@ -113,11 +113,12 @@ def test_noalloc_decode_per_sequence_lengths():
 
 
 def test_noalloc_decode_rejects_partials_beyond_scratch():
-    """A batch whose split-K partials exceed the library scratch is refused with EINVAL, before any launch."""
+    """A batch whose split-K partials exceed the library scratch is refused with EINVAL, before any launch.
+    The tensor pointers are NULL: the size check comes first, and were it ever moved after the
+    pointer checks, the call would still stop there (q is NULL) rather than launch."""
     lib = _native.lib()
     B, Hq, Hkv, L, D = 2048, 32, 32, 128, 256  # one split per head: 65536 x (4 + 256) fp32 > 32 MiB
     assert B * Hq * (4 + D) * 4 > _native.DECODE_SCRATCH_BYTES
-    P = 256  # never dereferenced: the size check comes first
-    rc = lib.co_alibi_decode_noalloc(1, P, P, P, P, None, P, None, B, Hq, Hkv, L, L, D, 0.1, None)
+    rc = lib.co_alibi_decode_noalloc(1, None, None, None, None, None, None, None, B, Hq, Hkv, L, L, D, 0.1, None)
     assert rc == 1
     assert "above the library scratch" in lib.co_alibi_last_error().decode()
