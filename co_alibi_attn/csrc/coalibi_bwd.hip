@@ -164,9 +164,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   const int col = lane & 31, hh = lane >> 5;
   const int Sq = args.Sq, Skv = args.Skv;
   const int nQB = (Sq + kBM - 1) / kBM;
-  const bool sorted = args.row_order != nullptr && (args.flags[0] & kFlagRowOrder) != 0;
+  // The fixed order rotates the heads over the XCDs when the tail skip made their work differ;
+  // with every head's work alike it keeps each head on one XCD, where its row blocks share the
+  // K / V tiles in L2 (full work: -4 % at the headline, measured).
+  const int flags = args.flags[0];
+  const bool sorted = args.row_order != nullptr && (flags & kFlagRowOrder) != 0;
   const WorkItem item = sorted ? table_item(args.row_order, blockIdx.x, args.B * args.Hq, gridDim.x)
-                               : lpt_item(blockIdx.x, args.B * args.Hq, 1);
+                               : lpt_item(blockIdx.x, args.B * args.Hq, (flags & kFlagTailSkip) ? 1 : 1 << 30);
   const int bh = item.head;
   const int qb = nQB - 1 - item.rank;  // rank 0: the longest causal rows
   const int b = bh / args.Hq, hq = bh - b * args.Hq;

@@ -618,6 +618,7 @@ hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
     // order, which the fixed orders of the kernels beat (their heads rotate over the XCDs).
     if (a.row_order != nullptr && rows_sorted) f.order_flags |= kFlagRowOrder;
     if (a.key_order != nullptr && keys_sorted) f.order_flags |= kFlagKeyOrder;
+    f.order_flags |= kFlagTailSkip;
   }
   if (a.knorm == nullptr || !rows_sorted) f.row_order = nullptr;  // no sorted table: the fixed order
   const int nQB = (a.Sq + kFwdBM - 1) / kFwdBM;

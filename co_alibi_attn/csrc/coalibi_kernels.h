@@ -13,8 +13,9 @@ constexpr float kLog2eHost = 1.4426950408889634f;
 // Statistics the forward saves for the backward besides LSE ("stats", int32 / fp32 words,
 // O(B*Hq*S) in all):
 //   header (kStatsHeader words): word 0 holds flags -- bit 0: row_order is a work order the
-//     key-norm launch wrote, bit 1: key_order likewise; without a bit the kernels that would
-//     read the table use their fixed order instead; the other header words are zero;
+//     key-norm launch wrote, bit 1: key_order likewise (without a bit the kernels that would
+//     read the table use their fixed order instead), bit 2: the forward ran with the tail
+//     skip; the other header words are zero;
 //   kstart (B*Hq, nQB) int32, nQB = ceil(Sq/128): the first key the forward processed for
 //     each 128-row block (0 when the tail skip is off).  Every key left of it has a softmax
 //     weight below 2^-skip_log2 of its row's total in every row of the block (the tail skip
@@ -51,6 +52,7 @@ constexpr float kLog2eHost = 1.4426950408889634f;
 constexpr int kStatsHeader = 4;
 constexpr int kFlagRowOrder = 1;
 constexpr int kFlagKeyOrder = 2;
+constexpr int kFlagTailSkip = 4;  // the forward ran with the tail skip
 constexpr int kNormKeys = 256;
 template <typename T>
 constexpr float skip_log2() {

@@ -109,8 +109,9 @@ def test_orders_are_sorted_permutations(case):
     stats, ws, o, o_inf = run_fwd(B, Hq, Hkv, Sq, Skv, D, dtype, causal, slopes.tolist())
     bh, nqb, nkc, nkb = B * Hq, -(-Sq // 128), -(-Skv // 256), -(-Skv // 64)
     ints = stats.view(torch.int32).numpy()
-    # header: the row table and, with one query head per key head, the key table are flagged
-    assert ints[0] == 1 | (2 if Hq == Hkv else 0) and not ints[1:4].any()
+    # header: the row table and, with one query head per key head, the key table are flagged, and
+    # so is the tail skip
+    assert ints[0] == 1 | (2 if Hq == Hkv else 0) | 4 and not ints[1:4].any()
     tail = 4 + bh * (nqb + nkc)
     rows = ints[tail: tail + bh * nqb]
     assert np.array_equal(np.sort(rows), np.arange(bh * nqb)), "row order is not a permutation"
