@@ -57,11 +57,11 @@ def _device_slopes(n_heads: int, bias_max: float, dtype: torch.dtype, device: to
     return slopes
 
 
-def _check_head_dim(head_dim: int, dtype: torch.dtype) -> None:
+def _check_head_dim(head_dim: int, dtype: torch.dtype, decode: bool = False) -> None:
     if head_dim not in _native.SUPPORTED_HEAD_DIMS:
         raise ValueError(f"head_dim must be one of {_native.SUPPORTED_HEAD_DIMS}, got {head_dim}")
-    if head_dim == 256 and dtype == torch.float32:
-        raise ValueError("head_dim 256 needs float16 or bfloat16 inputs")
+    if decode and head_dim == 256 and dtype == torch.float32:
+        raise ValueError("decode at head_dim 256 needs float16 or bfloat16 inputs")
 
 
 def _check_inputs(q, k, v, slopes) -> None:
@@ -170,7 +170,7 @@ def co_alibi_decode(q, k_cache, v_cache, seq_len=None, sm_scale=None, bias_max=8
             f"q and the caches must share one dtype of float32/float16/bfloat16, got "
             f"{q.dtype}, {k_cache.dtype}, {v_cache.dtype}"
         )
-    _check_head_dim(head_dim, q.dtype)
+    _check_head_dim(head_dim, q.dtype, decode=True)
     if sm_scale is None:
         sm_scale = 1.0 / (head_dim ** 0.5)
 

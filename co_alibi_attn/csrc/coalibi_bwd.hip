@@ -382,18 +382,22 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
 // 32-key block, held as MFMA A operands (row R <-> key kw0 + kRowOfReg(R)) so that
 // register r of lane (col, hh) of S^T <-> key kw0 + hh*16 + r, query q0 + sq*32 + col.
 // The 16-bit kernel below splits this work over wavefront pairs; fp32 tiles with
-// their transposed copies do not fit the LDS that split needs.
+// their transposed copies do not fit the LDS that split needs.  At D = 256 the fp32
+// transposed copies alone would not fit either: the reduction's Q^T / dO^T operands are
+// then read element by element from the row-major tiles (one 4-byte read per element,
+// the 32 lanes of a half reading 32 consecutive head-dim columns of one row).
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs args) {
   using C = BwdCfg<T, D>;
   using M = Mfma<T>;
   using vec8 = typename M::vec8;
   constexpr int BQ = kBQ<T>;
-  using Tile = TileLoader<T, D, BQ, !BwdCfg<T, D>::kTr>;
+  constexpr bool kCols = !C::kTr && D <= 128;  // transposed copies of the Q and dO tiles in LDS
+  using Tile = TileLoader<T, D, BQ, kCols>;
   __shared__ __align__(16) T sQ[BQ * C::LDR];
   __shared__ __align__(16) T sdO[BQ * C::LDR];
-  __shared__ __align__(16) T sQt[C::kTr ? 8 : C::DP * C::LDT2];
-  __shared__ __align__(16) T sdOt[C::kTr ? 8 : C::DP * C::LDT2];
+  __shared__ __align__(16) T sQt[kCols ? C::DP * C::LDT2 : 8];
+  __shared__ __align__(16) T sdOt[kCols ? C::DP * C::LDT2 : 8];
   __shared__ __align__(16) T sSP[4][2][32 * C::LDSP];  // per wavefront: s and dP, [q][key] (fp32: [key][q])
   __shared__ __align__(16) float sLse2[BQ];
   __shared__ __align__(16) float sDsum[BQ];
@@ -421,7 +425,7 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
   if constexpr (D < C::DP) {  // padding columns of Q and dO (read across d by phase B) stay zero
     lds_zero(sQ, (int)sizeof(sQ), tid, 256);
     lds_zero(sdO, (int)sizeof(sdO), tid, 256);
-    if constexpr (!C::kTr) {
+    if constexpr (kCols) {
       lds_zero(sQt, (int)sizeof(sQt), tid, 256);
       lds_zero(sdOt, (int)sizeof(sdOt), tid, 256);
     }
@@ -487,7 +491,7 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
     __syncthreads();
     qregs.template store_rows<false>(sQ, C::LDR, tid);
     doregs.template store_rows<false>(sdO, C::LDR, tid);
-    if constexpr (!C::kTr) {
+    if constexpr (kCols) {
       qregs.store_cols(sQt, C::LDT2, tid);
       doregs.store_cols(sdOt, C::LDT2, tid);
     }
@@ -563,9 +567,16 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
           if constexpr (C::kTr) {
             doa = ld_kmajor<T, false>(sdO, C::LDR, sq * 32 + mh * 16, 8, dt * 32, lane);
             qa = ld_kmajor<T, false>(sQ, C::LDR, sq * 32 + mh * 16, 8, dt * 32, lane);
-          } else {
+          } else if constexpr (kCols) {
             doa = ld_vec8(sdOt + (dt * 32 + col) * C::LDT2 + sq * 32 + mh * 16 + hh * 8);
             qa = ld_vec8(sQt + (dt * 32 + col) * C::LDT2 + sq * 32 + mh * 16 + hh * 8);
+          } else {
+            const int r0 = sq * 32 + mh * 16 + hh * 8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              doa[e] = sdO[(r0 + e) * C::LDR + dt * 32 + col];
+              qa[e] = sQ[(r0 + e) * C::LDR + dt * 32 + col];
+            }
           }
           dv[dt] = M::k16(doa, sop, dv[dt]);
           dk[dt] = M::k16(qa, pop, dk[dt]);
@@ -1145,5 +1156,6 @@ COALIBI_INST_BWD(float, 16)
 COALIBI_INST_BWD(float, 32)
 COALIBI_INST_BWD(float, 64)
 COALIBI_INST_BWD(float, 128)
+COALIBI_INST_BWD(float, 256)
 
 }  // namespace coalibi

@@ -65,10 +65,6 @@ int check_shape(const char* fn, int dtype, const Shape& s) {
   if (s.D != 16 && s.D != 32 && s.D != 64 && s.D != 128 && s.D != 256)
     return fail(CO_ALIBI_EUNSUPPORTED,
                 std::string(fn) + ": head_dim must be 16, 32, 64, 128 or 256, got " + std::to_string(s.D));
-  // fp32 tiles at D = 256 exceed the register file in backward pass 2 (fragments and
-  // accumulators of 32 keys x 256 dims in fp32).
-  if (s.D == 256 && dtype == CO_ALIBI_F32)
-    return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": head_dim 256 needs fp16 or bf16");
   // Sequence indices are 32-bit in the kernels; grids must fit a 31-bit launch.
   const double wg = std::ceil(s.Sq / 128.0) * s.B * s.Hq;
   if (s.Sq > (1 << 30) || s.Skv > (1 << 30) || wg > 2147483647.0)
@@ -101,9 +97,7 @@ hipError_t fwd_dispatch_d(const coalibi::FwdArgs& a, int D, bool causal, hipStre
     case 16: return fwd_dispatch_causal<T, 16>(a, causal, st);
     case 32: return fwd_dispatch_causal<T, 32>(a, causal, st);
     case 64: return fwd_dispatch_causal<T, 64>(a, causal, st);
-    case 256:
-      if constexpr (sizeof(T) == 2) return fwd_dispatch_causal<T, 256>(a, causal, st);
-      return hipErrorInvalidValue;
+    case 256: return fwd_dispatch_causal<T, 256>(a, causal, st);
     default: return fwd_dispatch_causal<T, 128>(a, causal, st);
   }
 }
@@ -119,9 +113,7 @@ hipError_t bwd_dispatch_d(const coalibi::BwdArgs& a, int D, bool causal, int sta
     case 16: return bwd_dispatch_causal<T, 16>(a, causal, stages, st);
     case 32: return bwd_dispatch_causal<T, 32>(a, causal, stages, st);
     case 64: return bwd_dispatch_causal<T, 64>(a, causal, stages, st);
-    case 256:
-      if constexpr (sizeof(T) == 2) return bwd_dispatch_causal<T, 256>(a, causal, stages, st);
-      return hipErrorInvalidValue;
+    case 256: return bwd_dispatch_causal<T, 256>(a, causal, stages, st);
     default: return bwd_dispatch_causal<T, 128>(a, causal, stages, st);
   }
 }
@@ -464,6 +456,10 @@ int decode_impl(const char* fn, bool scratch_ws, int dtype, const void* q, const
   if (head_dim == 16)
     return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": head_dim 16 has no decode kernel (pad q and the "
                                                          "caches to 32 with zeros)");
+  // A wavefront's K and V tiles (32 cache rows each) of fp32 at head dim 256 take 66 KB of LDS,
+  // four wavefronts more than a CU has.
+  if (head_dim == 256 && dtype == CO_ALIBI_F32)
+    return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": decode at head_dim 256 needs fp16 or bf16");
   if (heads_q / heads_kv > coalibi::kMaxDecodeGroup)
     return fail(CO_ALIBI_EUNSUPPORTED, std::string(fn) + ": at most " + std::to_string(coalibi::kMaxDecodeGroup) +
                                            " query heads per kv head");

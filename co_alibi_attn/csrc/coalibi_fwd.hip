@@ -648,5 +648,6 @@ COALIBI_INST_FWD(float, 16)
 COALIBI_INST_FWD(float, 32)
 COALIBI_INST_FWD(float, 64)
 COALIBI_INST_FWD(float, 128)
+COALIBI_INST_FWD(float, 256)
 
 }  // namespace coalibi

@@ -26,6 +26,8 @@
  * stream), allocates nothing, and returns CO_ALIBI_OK or an error code; the
  * message of the last failure on the calling thread is co_alibi_last_error().
  * Pointers to element data must be 16-byte aligned, fp32 arrays 4-byte aligned.
+ * Head dims 16, 32, 64, 128 and 256 in every dtype (the decode: 32 to 256, and 256 only
+ * in fp16 / bf16).
  */
 #ifndef CO_ALIBI_H
 #define CO_ALIBI_H
@@ -147,8 +149,8 @@ size_t co_alibi_decode_workspace_bytes(int batch, int heads_q, int seq_kv, int h
  * reference has no decode entry point: this is its forward, co_alibi_attention(q, k,
  * v, causal=False) (co_alibi_attn/co_alibi_attn.py:137-148), with Sq = 1 and the
  * caches cut to len_b rows; its top-left causal mask (co_alibi_fwd_kernel.py:80-90)
- * would show an Sq = 1 query only the first key.  At most 32 query heads per kv
- * head, seq_kv <= 2^21 (it sizes the grid and the workspace); workspace holds
+ * would show an Sq = 1 query only the first key.  Head dims 32 to 256 (256 in fp16 /
+ * bf16 only); at most 32 query heads per kv head, seq_kv <= 2^21 (it sizes the grid and the workspace); workspace holds
  * co_alibi_decode_workspace_bytes(...) bytes (256-byte aligned). */
 int co_alibi_decode(int dtype, const void* q, const void* k_cache, const void* v_cache,
                     const float* slopes, const int* seq_lens, void* o, float* lse,

@@ -100,7 +100,6 @@ def _fwd(lib, **over):
     (dict(lse=2), 1, "lse is not 4-byte aligned"),
     (dict(D=96), 2, "head_dim must be 16, 32, 64, 128 or 256"),
     (dict(D=8), 2, "head_dim must be 16, 32, 64, 128 or 256"),
-    (dict(D=256, dtype=0), 2, "head_dim 256 needs fp16 or bf16"),
     (dict(dtype=7), 2, "dtype must be"),
     (dict(Hq=3, Hkv=2), 1, "multiple of heads_kv"),
     (dict(Sq=0), 1, ">= 1"),
@@ -209,6 +208,7 @@ def _decode(lib, **over):
     (dict(Hq=6, Hkv=4), 1, "multiple of heads_kv"),
     (dict(D=80), 2, "head_dim must be 16, 32, 64, 128 or 256"),
     (dict(D=16), 2, "head_dim 16 has no decode kernel"),
+    (dict(D=256, dtype=0), 2, "decode at head_dim 256 needs fp16 or bf16"),
     (dict(L=0), 1, ">= 1"),
     (dict(scale=float("inf")), 1, "sm_scale must be finite"),
 ])
