@@ -377,6 +377,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 || D > 128) ? 1 : 2) void coal
   }
 }
 
+// Pass 2's rotation of the heads over the XCDs (balanced_item): runs of kLptRotateRanks key
+// blocks of a head share an XCD when the tail skip made the heads' work differ; without it
+// every key block of a head stays on one XCD, where they share the head's Q / dO tiles in L2
+// (full work: pass 2 -3 % at the headline, -6 % with grouped heads, measured).
+__device__ __forceinline__ int pass2_rotate(const BwdArgs& args) {
+  return (args.flags[0] & kFlagTailSkip) ? kLptRotateRanks : 1 << 30;
+}
+
 // ---------------------------------------------------------------------------
 // Pass 2, fp32 validation mode: dK, dV.  Per wavefront the 32 keys kw0.. of one
 // 32-key block, held as MFMA A operands (row R <-> key kw0 + kRowOfReg(R)) so that
@@ -411,7 +419,7 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
   static_assert(sizeof(sQ) >= 2 * kMaxBalancedHeads * 4, "the head order is built in sQ");
   const WorkItem item = balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
                                       reinterpret_cast<float*>(sQ), reinterpret_cast<int*>(sQ) + kMaxBalancedHeads,
-                                      tid, 256);
+                                      tid, 256, pass2_rotate(args));
   const int bhk = item.head;               // b * Hkv + hkv
   const int kb = item.rank;                // rank 0: key block 0, seen by the most query rows
   const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;
@@ -706,7 +714,8 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
       sorted ? table_item(args.key_order, blockIdx.x, args.B * args.Hkv, gridDim.x)
              : balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
                                      reinterpret_cast<float*>(&sSP[0][0][0]),
-                                     reinterpret_cast<int*>(&sSP[0][0][0]) + kMaxBalancedHeads, tid, 64 * kPairWaves);
+                                     reinterpret_cast<int*>(&sSP[0][0][0]) + kMaxBalancedHeads, tid, 64 * kPairWaves,
+                                     pass2_rotate(args));
   const int bhk = item.head;               // b * Hkv + hkv
   const int kb = item.rank;                // rank 0: key block 0, seen by the most query rows
   const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;
@@ -949,7 +958,8 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
   const WorkItem item = sorted ? table_item(args.key_order, blockIdx.x, args.B * args.Hkv, gridDim.x)
                                : balanced_item(blockIdx.x, args.B, args.Hkv, args.slopes, args.Hq / args.Hkv,
                                                reinterpret_cast<float*>(sQ[1]),
-                                               reinterpret_cast<int*>(sQ[1]) + kMaxBalancedHeads, tid, 256);
+                                               reinterpret_cast<int*>(sQ[1]) + kMaxBalancedHeads, tid, 256,
+                                               pass2_rotate(args));
   const int bhk = item.head;  // b * Hkv + hkv
   const int kb = item.rank;   // rank 0: key block 0, seen by the most query rows
   const int b = bhk / args.Hkv, hkv = bhk - b * args.Hkv;

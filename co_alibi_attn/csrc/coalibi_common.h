@@ -231,12 +231,15 @@ constexpr int kMaxBalancedHeads = 256;
 // `key` and `order` (kMaxBalancedHeads floats / ints of LDS scratch, free again on return)
 // hold the heads' slopes and rank order; every thread of the work-group calls this (three
 // barriers).
+// `rotate`: ranks per rotation step (kLptRotateRanks; without the tail skip every head has the
+// same work, and a rotate past the ranks keeps each head on one XCD).
 __device__ __forceinline__ WorkItem balanced_item(int id, int B, int H, const float* __restrict__ slopes,
-                                                  int group, float* key, int* order, int tid, int nthreads) {
+                                                  int group, float* key, int* order, int tid, int nthreads,
+                                                  int rotate) {
   const int heads = B * H;
   const int rank = id / heads;
   int j = id - rank * heads;
-  j = (j + rank / kLptRotateRanks) % heads;
+  j = (j + rank / rotate) % heads;
   if (H > kMaxBalancedHeads) return {j, rank};
   for (int t = tid; t < H; t += nthreads) {
     float m = __builtin_inff();
