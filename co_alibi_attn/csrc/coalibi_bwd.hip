@@ -459,10 +459,15 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
   const float tile_sc2 = sizeof(T) == 2 ? 1.0f : args.sc2;
 
   f32x16 dk[C::DT], dv[C::DT];
+  f32x16 ck[sizeof(T) == 4 ? C::DT : 1], cv[sizeof(T) == 4 ? C::DT : 1];  // fp32: the sums' compensations
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) {
     dk[dt] = f32x16{};
     dv[dt] = f32x16{};
+    if constexpr (sizeof(T) == 4) {
+      ck[dt] = f32x16{};
+      cv[dt] = f32x16{};
+    }
   }
 
   // Work list: (query head gi, query tile qt) pairs, prefetched one ahead.  Query tiles
@@ -561,19 +566,26 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
       }
       __builtin_amdgcn_sched_barrier(0);
       // dV^T[d][key] += dO^T[d][q] s[q][key];  dK^T[d][key] += Q^T[d][q] dP[q][key]
-      // reduction rows (queries) mh*16 + kh*8 + e of the subtile.
+      // reduction rows (queries) mh*16 + kh*8 + e of the subtile.  The subtile's 32 queries
+      // are summed in a fresh accumulator that is then added to the running one: one rounding
+      // at the running sum's magnitude per subtile instead of one per product step (in fp32
+      // a plain running dK / dV over a long grouped row range drifts by ~1e-4 at |dV| ~ 100).
+      vec8 sop[2], pop[2];
 #pragma unroll
       for (int mh = 0; mh < 2; ++mh) {
-        vec8 sop, pop;
         if constexpr (C::kTr) {
-          sop = ld_kmajor<T, false>(sS, C::LDSP, mh * 16, 8, 0, lane);
-          pop = ld_kmajor<T, false>(sP, C::LDSP, mh * 16, 8, 0, lane);
+          sop[mh] = ld_kmajor<T, false>(sS, C::LDSP, mh * 16, 8, 0, lane);
+          pop[mh] = ld_kmajor<T, false>(sP, C::LDSP, mh * 16, 8, 0, lane);
         } else {
-          sop = ld_vec8(sS + col * C::LDSP + mh * 16 + hh * 8);
-          pop = ld_vec8(sP + col * C::LDSP + mh * 16 + hh * 8);
+          sop[mh] = ld_vec8(sS + col * C::LDSP + mh * 16 + hh * 8);
+          pop[mh] = ld_vec8(sP + col * C::LDSP + mh * 16 + hh * 8);
         }
+      }
 #pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) {
+      for (int dt = 0; dt < C::DT; ++dt) {
+        f32x16 tv = f32x16{}, tk = f32x16{};
+#pragma unroll
+        for (int mh = 0; mh < 2; ++mh) {
           vec8 doa, qa;
           if constexpr (C::kTr) {
             doa = ld_kmajor<T, false>(sdO, C::LDR, sq * 32 + mh * 16, 8, dt * 32, lane);
@@ -589,8 +601,21 @@ __global__ __launch_bounds__(256, 1) void coalibi_bwd_dkdv_f32_kernel(BwdArgs ar
               qa[e] = sQ[(r0 + e) * C::LDR + dt * 32 + col];
             }
           }
-          dv[dt] = M::k16(doa, sop, dv[dt]);
-          dk[dt] = M::k16(qa, pop, dk[dt]);
+          tv = M::k16(doa, sop[mh], tv);
+          tk = M::k16(qa, pop[mh], tk);
+        }
+        if constexpr (sizeof(T) == 4) {
+          // fp32: compensated (Kahan) running sums, so the running dK / dV stay within a few
+          // ulps over any number of subtiles.
+          const f32x16 yv = tv - cv[dt], yk = tk - ck[dt];
+          const f32x16 sv = dv[dt] + yv, sk = dk[dt] + yk;
+          cv[dt] = (sv - dv[dt]) - yv;
+          ck[dt] = (sk - dk[dt]) - yk;
+          dv[dt] = sv;
+          dk[dt] = sk;
+        } else {
+          dv[dt] += tv;
+          dk[dt] += tk;
         }
       }
     }
