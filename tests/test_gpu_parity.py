@@ -628,6 +628,68 @@ def test_full_size_invariances(name):
         assert err <= TOL[w.dtype]
 
 
+# --------------------------------------------------------------------------- long sequences
+
+LONG_ROWS = [
+    # (S, D, dtype): two query heads on one key head (slopes 0.125 and 2^-7), past the BASELINE
+    # configs' 16384.  At 49152 the backward takes the score store (9.7 GB of records); at 2^17
+    # the records (69 GB) would pass the store's 16 GiB limit and it takes the recompute path
+    # (8.6 GB of zb / cb); fp32 runs its own kernels.
+    (49152, 64, torch.float16),
+    (131072, 64, torch.bfloat16),
+    (32768, 128, torch.float32),
+]
+
+
+@pytest.mark.parametrize("S,D,dtype", LONG_ROWS, ids=lambda x: str(x).split(".")[-1])
+def test_long_sequence_rows(S, D, dtype):
+    """Sequence lengths past the BASELINE configs, with the tail skip on and off.  The oracle
+    evaluates what it can afford at these lengths: O and dQ of three 64-row bands (the first, one
+    in the middle, the last: each row needs only its own keys), and dK / dV of the last 64 keys,
+    which only the last 64 rows see (causal).  Besides the bar of assert_parity, every output is
+    within 5 % of its largest reference magnitude (rows that average many keys have small
+    outputs).  Over the whole sequence, sum_j dV_j = sum_i dO_i (the weights of a row sum to 1)."""
+    Hq = 2
+    print(f"long sequence: B1 Hq{Hq} Hkv1 S{S} D{D} {dtype}", flush=True)
+    q, k, v, do = rand_inputs(1, Hq, 1, S, S, D, dtype, seed=S + D)
+    runs = {}
+    for skip in (True, False):
+        with _native.tail_skip(skip):
+            runs[skip] = hip_fwd_bwd(q, k, v, do)
+    do_sum = do.double().sum((1, 2))
+    for skip, got in runs.items():
+        rel = ((got[3].double().sum((1, 2)) - do_sum).abs().max() / do_sum.abs().max()).item()
+        print(f"  tail skip {skip}: sum_j dV_j vs sum_i dO_i: rel {rel:.2e}", flush=True)
+        assert rel < 1e-2
+    lam = ref.slopes(Hq, 8.0, dtype=dtype).float()
+    scale = 1.0 / math.sqrt(D)
+    kf, vf = k[0, 0].float(), v[0, 0].float()
+    bands = [(0, 64), (S // 2 - 32, S // 2 + 32), (S - 64, S)]
+    rows = torch.cat([torch.arange(r0, r1) for r0, r1 in bands])
+    want_o, want_dq = [], []
+    want_dk = torch.zeros(64, D)
+    want_dv = torch.zeros(64, D)
+    for h in range(Hq):
+        qf, dof = q[0, h].float(), do[0, h].float()
+        for r0, r1 in bands:
+            ob, *_ = ref._rows_forward(qf[r0:r1], kf[:r1], vf[:r1], lam[h], True, scale, r0)
+            dqb, dkb, dvb = ref._rows_backward(qf[r0:r1], dof[r0:r1], kf[:r1], vf[:r1], lam[h], True, scale, r0)
+            want_o.append(ob)
+            want_dq.append(dqb)
+        # The last band's contributions to the last 64 keys are their whole dK / dV from head h.
+        want_dk += dkb[S - 64:]
+        want_dv += dvb[S - 64:]
+    want = (torch.cat(want_o), torch.cat(want_dq), want_dk, want_dv)
+    for skip, (o, dq, dk, dv) in runs.items():
+        got = (o[0][:, rows].reshape(-1, D), dq[0][:, rows].reshape(-1, D), dk[0, 0, S - 64:], dv[0, 0, S - 64:])
+        label = f"S{S} D{D} (tail skip {'on' if skip else 'off'})"
+        assert_parity(got, want, TOL[dtype], label, dtype)
+        for n_, g_, w_ in zip(("o", "dq", "dk", "dv"), got, want):
+            rel = ((g_ - w_).abs().max() / w_.abs().max()).item()
+            print(f"  {label} {n_}: max-abs / max|ref| {rel:.2e}", flush=True)
+            assert rel <= 0.05, f"{label}: {n_} off by {rel:.1%} of its magnitude"
+
+
 # --------------------------------------------------------------------------- seeded random shapes
 
 def _random_cases(n=18, seed=2024):
