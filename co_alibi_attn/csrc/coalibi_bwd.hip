@@ -1021,10 +1021,17 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
 
   Dma dma;
   dma.init(wave, lane);
+  // Loop invariants kept in scalar registers: the LDS addresses of the tile buffers, the Q / dO
+  // of the group's first query head and the head stride.
+  const unsigned lds_q = lds_address(sQ[0]), lds_do = lds_address(sdO[0]);
+  const size_t head0 = (size_t)(b * args.Hq + hkv * group) * Sq * D, head_stride = (size_t)Sq * D;
+  const T* __restrict__ q_g = static_cast<const T*>(args.q) + head0;
+  const T* __restrict__ do_g = static_cast<const T*>(args.dout) + head0;
   auto issue_tile = [&](int gi, int qt, int buf) {
-    const size_t qoff = (size_t)(b * args.Hq + hkv * group + gi) * Sq * D;
-    dma.issue_untracked(static_cast<const T*>(args.q) + qoff, qt * BQ, Sq, sQ[buf], wave);
-    dma.issue_untracked(static_cast<const T*>(args.dout) + qoff, qt * BQ, Sq, sdO[buf], wave);
+    const size_t qoff = (size_t)gi * head_stride;
+    const unsigned lbuf = (unsigned)(buf * TILE * (int)sizeof(T));
+    dma.issue_untracked(q_g + qoff, qt * BQ, Sq, lds_q + lbuf, wave);
+    dma.issue_untracked(do_g + qoff, qt * BQ, Sq, lds_do + lbuf, wave);
   };
   // This wavefront's query half of tile qt holds visible pairs of its key group that the
   // forward processed: exactly the records pass 1 wrote.
@@ -1036,12 +1043,15 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
   };
   // The four operands of the record, 16 bytes per lane each; a record that is not live is
   // read through an empty resource (zeros, and no branch around the loads).
+  // Record of (query head gi, 32-row block qb): rec0 + gi * score_head + qb (records are key-block
+  // major, so the row blocks of one key block are consecutive).
+  const size_t rec0 =
+      (size_t)(b * args.Hq + hkv * group) * args.score_head + score_record(jb, jb, nQ32, CAUSAL) - (size_t)jb;
   auto load_record = [&](int gi, int qt, vec8 (&r)[4]) {
     const bool ok = live(gi, qt);
-    const size_t bh = (size_t)b * args.Hq + hkv * group + gi;
     const int qb = qt * 2 + qh;
     const char* base = static_cast<const char*>(args.scores) +
-                       (ok ? (bh * args.score_head + score_record(jb, qb, nQ32, CAUSAL)) * kScoreRecordBytes : 0);
+                       (ok ? (rec0 + (size_t)gi * args.score_head + (size_t)qb) * kScoreRecordBytes : 0);
     const __amdgpu_buffer_rsrc_t rs = tile_rsrc(reinterpret_cast<const u32x4*>(base), ok ? kScoreRecordBytes / 16 : 0);
 #pragma unroll
     for (int m = 0; m < 4; ++m)  // read once: non-temporal, as pass 1 wrote them

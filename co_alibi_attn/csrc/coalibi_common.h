@@ -132,18 +132,23 @@ __device__ __forceinline__ void dma16_to_lds(__amdgpu_buffer_rsrc_t rsrc, void* 
 // of a buffer before DMA into it is issued.  m0 holds the LDS base of the instruction.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16_to_lds_untracked(__amdgpu_buffer_rsrc_t rsrc, void* lds, int voffset) {
-  const unsigned a = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(__attribute__((address_space(3))) void*)lds);
+// `lds_byte` is the LDS byte address (wave-uniform), as lds_address() gives it.
+__device__ __forceinline__ void dma16_to_lds_untracked(__amdgpu_buffer_rsrc_t rsrc, unsigned lds_byte, int voffset) {
   asm volatile(
       "s_nop 4\n\t"
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
       "buffer_load_dwordx4 %1, %2, 0 offen lds"
       :
-      : "s"(a), "v"(voffset), "s"(rsrc)
+      : "s"(lds_byte), "v"(voffset), "s"(rsrc)
       : "memory", "m0");
 }
 #pragma clang diagnostic pop
+// The LDS byte address of a pointer into LDS, wave-uniform.  The conversion from a generic
+// pointer tests it for null (scalar instructions): a loop takes it once, outside.
+__device__ __forceinline__ unsigned lds_address(const void* lds) {
+  return __builtin_amdgcn_readfirstlane((unsigned)(size_t)(const __attribute__((address_space(3))) void*)lds);
+}
 // The same with the non-temporal cache policy (the "nt" bit, cache-policy value 2), for data
 // read exactly once: a stream of such loads sustains about 15 % more HBM bandwidth on
 // MI355X (6.9 against 6.0 TB/s in a read-only test of this access pattern).
@@ -288,6 +293,7 @@ struct DmaTile {
   static constexpr int NINSTR = (ROWS * CPR + 63) / 64;  // wavefront DMA instructions per tile
   static constexpr int LDS_ELEMS = NINSTR * 64 * CH;     // LDS the tile's instructions write
   static constexpr int SLOTS = (NINSTR + NWAVES - 1) / NWAVES;
+  static_assert(NWAVES * (SLOTS - 1) < NINSTR, "every slot but the last holds an instruction");
   static_assert(LD * (int)sizeof(T) % 16 == 0 && LD >= D, "rows must be whole 16-byte chunks");
   static_assert(!PERM || ROWS % 32 == 0, "rows are permuted in blocks of 32");
   int off[SLOTS];
@@ -309,13 +315,16 @@ struct DmaTile {
       if (i < NINSTR) dma16_to_lds(rsrc, lds + i * 64 * 16 / (int)sizeof(T), off[m]);
     }
   }
-  // The same through dma16_to_lds_untracked (its rules apply).
-  __device__ __forceinline__ void issue_untracked(const T* base, int row0, int nrows, T* lds, int wave) const {
+  // The same through dma16_to_lds_untracked (its rules apply), into the tile at LDS byte
+  // address lds_byte (lds_address).  wave < NWAVES, so only the last slot can lie past the
+  // tile's instructions.
+  __device__ __forceinline__ void issue_untracked(const T* base, int row0, int nrows, unsigned lds_byte,
+                                                  int wave) const {
     const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(base + (size_t)row0 * D, min(max(nrows - row0, 0), ROWS) * D);
 #pragma unroll
     for (int m = 0; m < SLOTS; ++m) {
       const int i = wave + NWAVES * m;
-      if (i < NINSTR) dma16_to_lds_untracked(rsrc, lds + i * 64 * 16 / (int)sizeof(T), off[m]);
+      if (m + 1 < SLOTS || i < NINSTR) dma16_to_lds_untracked(rsrc, lds_byte + i * 64 * 16, off[m]);
     }
   }
 };
