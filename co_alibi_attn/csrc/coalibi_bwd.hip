@@ -955,7 +955,10 @@ __global__ __launch_bounds__(64 * kPairWaves, D > 128 ? 1 : 2) void coalibi_bwd_
 constexpr int kStoreBK = 64;  // keys per work-group
 constexpr int kStoreBQ = 64;  // query rows per tile
 
-template <typename T, int D, bool CAUSAL>
+// LISTED: the key block's work items fit kStoreProcessedWords (group * query tiles, checked by
+// the launcher); they are then listed in LDS once, in walk order, each with its row block's
+// processed bit, in place of the per-head bit words and the walk in the loop.
+template <typename T, int D, bool CAUSAL, bool LISTED>
 __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs args) {
   static_assert(sizeof(T) == 2 && (D == 64 || D == 128), "the score store path is 16-bit, D 64 or 128");
   using C = BwdCfg<T, D>;
@@ -1004,14 +1007,33 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
   const int* __restrict__ kstart_g = args.kstart + (size_t)(b * args.Hq + hkv * group) * nSkipQB;
   const KeyBlockWork work = key_block_work<BQ>(sQtHi, kstart_g, group, Sq, Skv, qt0, kwg0, wave, 4, lane);
   const int wph = (nSkipQB + 63) / 64 * 2;  // words per head (the host checks group * wph fits)
-  for (int g = wave; g < group; g += 4) {
-    for (int rb0 = 0; rb0 < nSkipQB; rb0 += 64) {
-      const int rb = rb0 + lane;
-      const unsigned long long m =
-          __ballot(rb < nSkipQB && valid_kstart(kstart_g[(size_t)g * nSkipQB + rb], Skv) <= kwg0);
-      if (lane == 0) {
-        sProc[g * wph + rb0 / 32] = static_cast<unsigned>(m);
-        sProc[g * wph + rb0 / 32 + 1] = static_cast<unsigned>(m >> 32);
+  if constexpr (LISTED) {
+    __syncthreads();  // sQtHi
+    // Item i of the walk: query head gi, tile qt (from qt_hi(gi) down to qt0), as
+    // gi << 16 | qt << 1 | processed.
+    for (int i = tid; i < kStoreProcessedWords; i += 256) {
+      int gi = 0, base = 0;
+      for (; gi < group; ++gi) {
+        const int n = max(work.qt_hi(gi) - qt0 + 1, 0);
+        if (i < base + n) break;
+        base += n;
+      }
+      if (gi < group) {
+        const int qt = work.qt_hi(gi) - (i - base);
+        const bool proc = valid_kstart(kstart_g[(size_t)gi * nSkipQB + qt / 2], Skv) <= kwg0;
+        sProc[i] = (unsigned)gi << 16 | (unsigned)qt << 1 | (proc ? 1u : 0u);
+      }
+    }
+  } else {
+    for (int g = wave; g < group; g += 4) {
+      for (int rb0 = 0; rb0 < nSkipQB; rb0 += 64) {
+        const int rb = rb0 + lane;
+        const unsigned long long m =
+            __ballot(rb < nSkipQB && valid_kstart(kstart_g[(size_t)g * nSkipQB + rb], Skv) <= kwg0);
+        if (lane == 0) {
+          sProc[g * wph + rb0 / 32] = static_cast<unsigned>(m);
+          sProc[g * wph + rb0 / 32 + 1] = static_cast<unsigned>(m >> 32);
+        }
       }
     }
   }
@@ -1033,13 +1055,25 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
     dma.issue_untracked(q_g + qoff, qt * BQ, Sq, lds_q + lbuf, wave);
     dma.issue_untracked(do_g + qoff, qt * BQ, Sq, lds_do + lbuf, wave);
   };
+  // A work item: query head gi, query tile qt, and whether the forward processed this key block
+  // for the tile's row block.
+  struct Item {
+    int gi, qt;
+    bool proc;
+  };
+  auto walked = [&](int gi, int qt) {
+    const int rb = qt / 2;
+    return Item{gi, qt, ((sProc[gi * wph + rb / 32] >> (rb % 32)) & 1u) != 0};
+  };
+  auto listed = [&](int i) {
+    const unsigned e = __builtin_amdgcn_readfirstlane(sProc[i]);
+    return Item{(int)(e >> 16), (int)((e >> 1) & 0x7fffu), (e & 1u) != 0};
+  };
   // This wavefront's query half of tile qt holds visible pairs of its key group that the
   // forward processed: exactly the records pass 1 wrote.
-  auto live = [&](int gi, int qt) {
-    const int qs0 = qt * BQ + qh * 32;
-    const int rb = qt / 2;
-    return ((sProc[gi * wph + rb / 32] >> (rb % 32)) & 1u) != 0 && keys_ok && qs0 < Sq &&
-           (!CAUSAL || qs0 + 31 >= kw0);
+  auto live = [&](const Item& it) {
+    const int qs0 = it.qt * BQ + qh * 32;
+    return it.proc && keys_ok && qs0 < Sq && (!CAUSAL || qs0 + 31 >= kw0);
   };
   // The four operands of the record, 16 bytes per lane each; a record that is not live is
   // read through an empty resource (zeros, and no branch around the loads).
@@ -1047,11 +1081,10 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
   // major, so the row blocks of one key block are consecutive).
   const size_t rec0 =
       (size_t)(b * args.Hq + hkv * group) * args.score_head + score_record(jb, jb, nQ32, CAUSAL) - (size_t)jb;
-  auto load_record = [&](int gi, int qt, vec8 (&r)[4]) {
-    const bool ok = live(gi, qt);
-    const int qb = qt * 2 + qh;
+  auto load_record = [&](const Item& it, bool ok, vec8 (&r)[4]) {
+    const int qb = it.qt * 2 + qh;
     const char* base = static_cast<const char*>(args.scores) +
-                       (ok ? (rec0 + (size_t)gi * args.score_head + (size_t)qb) * kScoreRecordBytes : 0);
+                       (ok ? (rec0 + (size_t)it.gi * args.score_head + (size_t)qb) * kScoreRecordBytes : 0);
     const __amdgpu_buffer_rsrc_t rs = tile_rsrc(reinterpret_cast<const u32x4*>(base), ok ? kScoreRecordBytes / 16 : 0);
 #pragma unroll
     for (int m = 0; m < 4; ++m)  // read once: non-temporal, as pass 1 wrote them
@@ -1065,28 +1098,41 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
     dv[i] = f32x16{};
   }
   vec8 ra[4], rb[4];
-  int gi = work.next_head(0), qt = gi < group ? work.qt_hi(gi) : 0;  // current item
-  int gn = gi, qn = qt;                                                // next item
+  // The walk (without the list): heads in order, each head's tiles from qt_hi down to qt0.
+  int gn = work.next_head(0), qn = gn < group ? work.qt_hi(gn) : 0;
   auto advance = [&]() {
     const bool wrap = qn == qt0;
     const int g2 = wrap ? work.next_head(gn + 1) : gn;
     qn = wrap ? (g2 < group ? work.qt_hi(g2) : 0) : qn - 1;
     gn = g2;
   };
+  auto item_at = [&](int i) {  // item i; without the list, called for i = 0, 1, 2, ... in turn
+    if constexpr (LISTED) {
+      return listed(i);
+    } else {
+      const Item it = walked(gn, qn);
+      if (i + 1 < nwork) advance();
+      return it;
+    }
+  };
+  bool use = false;  // the current item is live for this wavefront
   if (nwork > 0) {
-    issue_tile(gi, qt, 0);
-    load_record(gi, qt, ra);
-    advance();
+    const Item it = item_at(0);
+    use = live(it);
+    issue_tile(it.gi, it.qt, 0);
+    load_record(it, use, ra);
   }
-  // Tile w: its Q / dO in buffer w & 1, its record in `cur`; the next item (gn, qn) is
-  // fetched into the other buffer and `nxt`.
+  // Tile w: its Q / dO in buffer w & 1, its record in `cur`; the next item is fetched into the
+  // other buffer and `nxt`.
   auto step = [&](int w, vec8 (&cur)[4], vec8 (&nxt)[4]) {
     __builtin_amdgcn_s_waitcnt(0);  // this wavefront's DMA and record loads of tile w
     __syncthreads();                // every wavefront's DMA of tile w; tile w - 1 no longer read
-    const bool use = live(gi, qt);
+    bool use_next = false;
     if (w + 1 < nwork) {
-      issue_tile(gn, qn, (w + 1) & 1);
-      load_record(gn, qn, nxt);
+      const Item it = item_at(w + 1);
+      use_next = live(it);
+      issue_tile(it.gi, it.qt, (w + 1) & 1);
+      load_record(it, use_next, nxt);
     }
     if (use) {
       const T* __restrict__ tQ = sQ[w & 1];
@@ -1102,9 +1148,7 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
         }
       }
     }
-    gi = gn;
-    qt = qn;
-    if (w + 1 < nwork) advance();
+    use = use_next;
   };
   for (int w = 0; w < nwork; w += 2) {
     step(w, ra, rb);
@@ -1168,8 +1212,13 @@ hipError_t launch_bwd(const BwdArgs& a, int stages, hipStream_t stream) {
     if (store) {
       if constexpr (kStore) {
         const int nKB = (a.Skv + kStoreBK - 1) / kStoreBK;
-        hipLaunchKernelGGL((coalibi_bwd_dkdv_store_kernel<T, D, CAUSAL>), dim3(nKB * a.B * a.Hkv), dim3(256), 0,
-                           stream, a);
+        const int nQT = (a.Sq + kStoreBQ - 1) / kStoreBQ;
+        if (static_cast<long long>(a.Hq / a.Hkv) * nQT <= kStoreProcessedWords)
+          hipLaunchKernelGGL((coalibi_bwd_dkdv_store_kernel<T, D, CAUSAL, true>), dim3(nKB * a.B * a.Hkv), dim3(256),
+                             0, stream, a);
+        else
+          hipLaunchKernelGGL((coalibi_bwd_dkdv_store_kernel<T, D, CAUSAL, false>), dim3(nKB * a.B * a.Hkv),
+                             dim3(256), 0, stream, a);
       }
     } else if constexpr (sizeof(T) == 2 && D >= 64) {  // the pair kernel splits D into 32-row halves
       const int nKB = (a.Skv + kPairBK - 1) / kPairBK;
