@@ -972,9 +972,9 @@ __global__ __launch_bounds__(256, 2) void coalibi_bwd_dkdv_store_kernel(BwdArgs 
   __shared__ __align__(16) T sdO[2][TILE];
   __shared__ int sQtHi[kMaxPairGroup];
   // Whether the forward processed this key block for row block rb of query head g: bit rb % 32
-  // of word g * wph + rb / 32 (kstart copied once, before any untracked DMA: loads after those
-  // cannot be proven unclobbered and would go through the vector memory counter, whose waits
-  // would also wait for the DMA).
+  // of word g * wph + rb / 32, or with LISTED the work items (kstart copied once, before any
+  // untracked DMA: loads after those cannot be proven unclobbered and would go through the
+  // vector memory counter, whose waits would also wait for the DMA).
   __shared__ unsigned sProc[kStoreProcessedWords];
   // The end-of-block exchange: 2 key groups x DT*16 accumulators x 64 lanes per half.
   static_assert(2 * C::DT * 16 * 64 * sizeof(float) <= sizeof(sQ), "the exchange fits one tile pair");
